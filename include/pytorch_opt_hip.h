@@ -1,0 +1,122 @@
+/*
+ * pytorch_opt_hip.h — C ABI of the MI355X (gfx950) backend for pytorch_opt.ops.
+ *
+ * One shared library, libpytorch_opt_hip.so, built from the .hip sources in
+ * pytorch-opt_amd/csrc. It replaces the reference's compiled
+ * backend object `_NATIVE` (pytorch_opt/ops/__init__.py:18, built by
+ * pytorch_opt/ops/native_build.py:10-21 from
+ * pytorch_opt/ops/csrc/pytorch_opt_ops.cpp). The Python adapter
+ * (pytorch_opt/ops/_hip.py) turns tensors into the plain pointers below.
+ *
+ * Conventions for every compute entry point:
+ *  - Pointers are device pointers to contiguous row-major data. Batched
+ *    arguments are `batch` matrices laid out back to back.
+ *  - `dtype` is one of PTO_F32, PTO_F64, PTO_BF16.
+ *  - `workspace` is caller-owned device memory of at least the size the
+ *    matching *_workspace_bytes query returns. The library never allocates
+ *    device memory and keeps no state between calls.
+ *  - `stream` is a hipStream_t; all kernels are enqueued on it and the call
+ *    returns without synchronising, except pto_inverse_root, which reads
+ *    its stop flag back once per chunk of iterations (the reference syncs
+ *    once per iteration: csrc/pytorch_opt_ops.cpp:29).
+ *  - Return value 0 means success. A non-zero value means failure, and
+ *    pto_last_error() returns a message (thread-local).
+ */
+#ifndef PYTORCH_OPT_HIP_H_
+#define PYTORCH_OPT_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { PTO_F32 = 0, PTO_F64 = 1, PTO_BF16 = 2 };
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* pto_last_error(void);
+/* Library version as major*10000 + minor*100 + patch. */
+int pto_version(void);
+/* HIP runtime version the library is bound to, or -1. */
+int pto_runtime_version(void);
+
+/*
+ * Newton–Schulz orthogonalization. Replaces
+ *   _NATIVE.newton_schulz_orthogonalize(G, steps, a, b, c, eps)
+ * called at pytorch_opt/ops/__init__.py:70; semantics of
+ * pytorch_opt/ops/reference.py:71-97 and csrc/pytorch_opt_ops.cpp:65-81.
+ * G and out are [batch, rows, cols] of `dtype`. bf16 computes with bf16
+ * operands and fp32 accumulation; f32/f64 stay in their own precision.
+ */
+size_t pto_ns5_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_t cols);
+int pto_ns5(const void* G, void* out, int dtype, int64_t batch, int64_t rows, int64_t cols, int64_t steps,
+            double a, double b, double c, double eps, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * In-place Kronecker factor update. Replaces
+ *   _NATIVE.kron_factor_update_(L, R, G, beta2)
+ * called at pytorch_opt/ops/__init__.py:76; semantics of
+ * pytorch_opt/ops/reference.py:100-114 and csrc/pytorch_opt_ops.cpp:83-94:
+ *   L <- beta2*L + (1-beta2)*G*G^T,  R <- beta2*R + (1-beta2)*G^T*G
+ * (beta2 == 1: L += G*G^T, R += G^T*G). G [m,n], L [m,m], R [n,n].
+ */
+size_t pto_kron_workspace_bytes(int dtype, int64_t m, int64_t n);
+int pto_kron_factor_update(void* L, void* R, const void* G, int dtype, int64_t m, int64_t n, double beta2,
+                           void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Gram update F <- beta*F + alpha * Xa^T Xa, Xa = [X, 1] if append_ones.
+ * The reference has no compiled counterpart: it is the boundary added for
+ * the K-FAC factor products pytorch_opt/curvature/kron.py:105-113 and the
+ * EMA / running-mean step :95-103 (beta == 0 overwrites F).
+ * X [rows, d] of x_dtype, F [d(+1), d(+1)] of f_dtype.
+ * Supported (x, F) pairs: (bf16, f32), (f32, f32), (f64, f64).
+ */
+size_t pto_gram_workspace_bytes(int x_dtype, int64_t rows, int64_t d, int append_ones);
+int pto_gram_update(void* F, int f_dtype, const void* X, int x_dtype, int64_t rows, int64_t d, int append_ones,
+                    double beta, double alpha, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Inverse p-th root by the coupled Newton iteration. Replaces the "newton"
+ * method of _NATIVE.inverse_matrix_root(A, p, damping, method, root_f64,
+ * max_iter, tol) called at pytorch_opt/ops/__init__.py:61-62; semantics of
+ * pytorch_opt/ops/reference.py:17-40,43-68 and csrc/pytorch_opt_ops.cpp:15-63.
+ * A and out are [batch, n, n] of `dtype`; the iteration runs in f64 if
+ * root_f64 else f32. *iters_out (may be NULL) receives the number of loop
+ * iterations executed.
+ */
+size_t pto_inverse_root_workspace_bytes(int root_f64, int64_t batch, int64_t n, int64_t max_iter);
+int pto_inverse_root(const void* A, void* out, int dtype, int root_f64, int64_t batch, int64_t n, int64_t p,
+                     double damping, int64_t max_iter, double tol, void* workspace, size_t ws_bytes,
+                     int64_t* iters_out, void* stream);
+
+/*
+ * Two-sided preconditioner application. Replaces
+ *   _NATIVE.precond_apply_two_sided(L_root, G, R_root)
+ * called at pytorch_opt/ops/__init__.py:83; semantics of
+ * pytorch_opt/ops/reference.py:117-121: out = (L_root*G)*R_root.
+ * L_root [m,m], G [m,n], R_root [n,n], out [m,n].
+ */
+size_t pto_precond_apply_workspace_bytes(int dtype, int64_t m, int64_t n);
+int pto_precond_apply(const void* L_root, const void* G, const void* R_root, void* out, int dtype, int64_t m,
+                      int64_t n, void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Kernel timing with HIP events. The reference has no counterpart (its
+ * StepTimer, pytorch_opt/optim/_common.py:82-98, is host wall-clock). While
+ * enabled, every MFMA launch is bracketed by events on its stream;
+ * pto_prof_query waits for them and returns the summed milliseconds and
+ * launch count for one kernel class ("ns5_gram", "ns5_square",
+ * "ns5_update", "kron_left", "kron_right", "gram_update", "root_xmi",
+ * "root_pow", "root_mk", "apply_left", "apply_right").
+ */
+int pto_prof_enable(int on);
+int pto_prof_reset(void);
+int pto_prof_query(const char* name, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PYTORCH_OPT_HIP_H_ */

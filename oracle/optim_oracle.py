@@ -1,0 +1,72 @@
+"""CPU oracle for the optimizer steps that drive the hot path — TEST
+INFRASTRUCTURE ONLY (used by tests/ and bench.py's cpu_baseline leg).
+
+numpy restatements of one Muon step (pytorch_opt/optim/muon.py:60-102),
+the shared AdamW fallback (pytorch_opt/optim/_common.py:56-79) and one
+Shampoo step for a single matrix parameter
+(pytorch_opt/optim/shampoo.py:70-160), used for teacher-forced checks:
+given the state a GPU run reached, the oracle computes the next state.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import ops_oracle as oo
+
+
+def muon_matrix_step(p, g, buf, lr=0.02, momentum=0.95, nesterov=True, ns_steps=5, weight_decay=0.0,
+                     lr_adjust="spectral"):
+    """One Muon update of a routed matrix; returns (p_new, buf_new, O)."""
+    buf = buf * np.float32(momentum) + g
+    u = g + np.float32(momentum) * buf if nesterov else buf
+    u2 = u if u.ndim == 2 else u.reshape(u.shape[0], -1)
+    O = oo.ns5(u2, steps=ns_steps).astype(np.float32)
+    rows, cols = O.shape[-2], O.shape[-1]
+    if lr_adjust == "spectral":
+        scale = max(1.0, rows / cols) ** 0.5
+    elif lr_adjust == "match_rms_adam":
+        scale = 0.2 * max(rows, cols) ** 0.5
+    else:
+        scale = 1.0
+    if weight_decay:
+        p = p * np.float32(1.0 - lr * weight_decay)
+    p = p - np.float32(lr * scale) * O.reshape(p.shape)
+    return p, buf, O
+
+
+def adamw_step(p, g, m, v, t, lr, betas=(0.9, 0.95), eps=1e-8, wd=0.0):
+    """One AdamW fallback step at step count t (1-based); returns (p, m, v)."""
+    b1, b2 = betas
+    m = m + np.float32(1 - b1) * (g - m)
+    v = v * np.float32(b2) + np.float32(1 - b2) * g * g
+    bc1, bc2 = 1 - b1 ** t, 1 - b2 ** t
+    denom = np.sqrt(v) / np.float32(bc2 ** 0.5) + np.float32(eps)
+    upd = (m / np.float32(bc1)) / denom
+    p = p * np.float32(1 - lr * wd) - np.float32(lr) * upd
+    return p, m, v
+
+
+def shampoo_matrix_step(p, g, L, R, L_root, R_root, graft_acc, step, factor_updates, lr=0.03, beta2=0.999,
+                        eps=1e-8, precondition_frequency=20, graft="adagrad", diag_eps=1e-10, root_dtype=np.float64,
+                        root_method="auto"):
+    """One Shampoo update of a selected matrix (no momentum / wd / bootstrap).
+
+    Returns the new (p, L, R, L_root, R_root, graft_acc).
+    """
+    g2 = g.reshape(g.shape[0], -1)
+    L, R = oo.kron_factor_update(L, R, g2, beta2)
+    factor_updates += 1
+    if step % precondition_frequency == 0:
+        bc = 1.0 - beta2 ** factor_updates if beta2 < 1.0 else 1.0
+        L_root = oo.inverse_root(L / np.float32(bc), 4, damping=eps, method=root_method, root_dtype=root_dtype)[0]
+        R_root = oo.inverse_root(R / np.float32(bc), 4, damping=eps, method=root_method, root_dtype=root_dtype)[0]
+    P = oo.precond_apply(L_root, g2, R_root)
+    if graft == "adagrad":
+        graft_acc = graft_acc + g2 * g2
+        target = np.linalg.norm(g2 / (np.sqrt(graft_acc) + np.float32(diag_eps)))
+        P = P * np.float32(target / (np.linalg.norm(P) + 1e-30))
+    elif graft == "sgd":
+        P = P * np.float32(np.linalg.norm(g2) / (np.linalg.norm(P) + 1e-30))
+    p = p - np.float32(lr) * P.reshape(p.shape)
+    return p, L, R, L_root, R_root, graft_acc

@@ -1,0 +1,184 @@
+// Memory-bound helper kernels shared by the op drivers: deterministic
+// per-matrix sums of squares, LDS-tiled pack/transpose with scaling and
+// zero padding, pad clearing and fills. None of these use hipMemset*, so
+// every op stays safe to record into a HIP graph.
+#pragma once
+
+#include <algorithm>
+
+#include "pto_common.h"
+
+namespace pto {
+
+constexpr int kRedBlocks = 64;  // partial sums per matrix
+
+// partial[b][blk] = sum of x^2 over a strided slice of matrix b (double).
+template <typename T>
+__global__ void __launch_bounds__(256) sumsq_partial_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+                                                            int64_t ld, int64_t sb, double* __restrict__ partial) {
+  const int b = blockIdx.y;
+  const T* xb = x + (int64_t)b * sb;
+  const int64_t total = rows * cols;
+  double s = 0.0;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = e / cols, c = e - r * cols;
+    double v = to_f(xb[r * ld + c]);
+    s += v * v;
+  }
+  __shared__ double red[256];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partial[(int64_t)b * gridDim.x + blockIdx.x] = red[0];
+}
+
+template <typename T>
+int launch_sumsq(const T* x, int64_t rows, int64_t cols, int64_t ld, int64_t sb, int batch, double* partial,
+                 hipStream_t stream) {
+  if (batch == 0) return 0;
+  hipLaunchKernelGGL(sumsq_partial_kernel<T>, dim3(kRedBlocks, batch), dim3(256), 0, stream, x, rows, cols, ld, sb,
+                     partial);
+  PTO_LAUNCHED("sumsq_partial");
+  return 0;
+}
+
+// out(r, c) = s_b * in(r, c) into a straight copy S and/or a transposed copy
+// Tt, both padded: S is [rows][ld_s] with cols..ld_s zero, Tt is
+// [cols + ones][ld_t] with rows..ld_t zero. If `ones` is set, Tt gets an
+// extra row (index cols) equal to 1 for r < rows (an appended ones column
+// of the input). scale == nullptr means s_b = 1.
+template <typename TI, typename TO, typename S>
+__global__ void __launch_bounds__(256) pack_kernel(const TI* __restrict__ in, int64_t rows, int64_t cols, int64_t ld_in,
+                                                   int64_t s_in, const S* __restrict__ scale, TO* __restrict__ out_s,
+                                                   int64_t ld_s, int64_t s_s, TO* __restrict__ out_t, int64_t ld_t,
+                                                   int64_t s_t, int ones) {
+  __shared__ float tile[64][65];
+  const int b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const TI* ib = in + (int64_t)b * s_in;
+  const S sc = scale ? scale[b] : S(1);
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  // Read the (r0, c0) tile of the input, coalesced along c.
+  for (int rr = ty; rr < 64; rr += 4) {
+    int64_t r = r0 + rr, c = c0 + tx;
+    float v = 0.f;
+    if (r < rows && c < cols) v = static_cast<float>(static_cast<S>(to_f(ib[r * ld_in + c])) * sc);
+    else if (ones && r < rows && c == cols) v = 1.f;
+    tile[rr][tx] = v;
+  }
+  __syncthreads();
+  if (out_s) {
+    TO* ob = out_s + (int64_t)b * s_s;
+    for (int rr = ty; rr < 64; rr += 4) {
+      int64_t r = r0 + rr, c = c0 + tx;
+      if (r < rows && c < ld_s) ob[r * ld_s + c] = static_cast<TO>(c < cols ? tile[rr][tx] : 0.f);
+    }
+  }
+  if (out_t) {
+    TO* ob = out_t + (int64_t)b * s_t;
+    const int64_t trows = cols + (ones ? 1 : 0);
+    for (int cc = ty; cc < 64; cc += 4) {
+      int64_t c = c0 + cc, r = r0 + tx;  // output row c, output column r
+      if (c < trows && r < ld_t) ob[c * ld_t + r] = static_cast<TO>(r < rows ? tile[tx][cc] : 0.f);
+    }
+  }
+}
+
+// Same as pack_kernel but exact for double data (the float tile would round).
+template <typename TI, typename TO, typename S>
+__global__ void __launch_bounds__(256) pack_kernel_f64(const TI* __restrict__ in, int64_t rows, int64_t cols,
+                                                       int64_t ld_in, int64_t s_in, const S* __restrict__ scale,
+                                                       TO* __restrict__ out_s, int64_t ld_s, int64_t s_s,
+                                                       TO* __restrict__ out_t, int64_t ld_t, int64_t s_t, int ones) {
+  __shared__ double tile[64][65];
+  const int b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const TI* ib = in + (int64_t)b * s_in;
+  const S sc = scale ? scale[b] : S(1);
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int rr = ty; rr < 64; rr += 4) {
+    int64_t r = r0 + rr, c = c0 + tx;
+    double v = 0.0;
+    if (r < rows && c < cols) v = static_cast<double>(static_cast<S>(to_f(ib[r * ld_in + c])) * sc);
+    else if (ones && r < rows && c == cols) v = 1.0;
+    tile[rr][tx] = v;
+  }
+  __syncthreads();
+  if (out_s) {
+    TO* ob = out_s + (int64_t)b * s_s;
+    for (int rr = ty; rr < 64; rr += 4) {
+      int64_t r = r0 + rr, c = c0 + tx;
+      if (r < rows && c < ld_s) ob[r * ld_s + c] = convert<TO>(c < cols ? tile[rr][tx] : 0.0);
+    }
+  }
+  if (out_t) {
+    TO* ob = out_t + (int64_t)b * s_t;
+    const int64_t trows = cols + (ones ? 1 : 0);
+    for (int cc = ty; cc < 64; cc += 4) {
+      int64_t c = c0 + cc, r = r0 + tx;
+      if (c < trows && r < ld_t) ob[c * ld_t + r] = convert<TO>(r < rows ? tile[tx][cc] : 0.0);
+    }
+  }
+}
+
+// Host wrapper. The grid covers the padded extents of both outputs.
+template <typename TI, typename TO, typename S>
+int launch_pack(const TI* in, int64_t rows, int64_t cols, int64_t ld_in, int64_t s_in, const S* scale, TO* out_s,
+                int64_t ld_s, int64_t s_s, TO* out_t, int64_t ld_t, int64_t s_t, bool ones, int batch,
+                hipStream_t stream) {
+  if (batch == 0) return 0;
+  int64_t rext = rows, cext = cols + (ones ? 1 : 0);
+  if (out_s) cext = std::max<int64_t>(cext, ld_s);
+  if (out_t) rext = std::max<int64_t>(rext, ld_t);
+  dim3 grid((unsigned)((cext + 63) / 64), (unsigned)((rext + 63) / 64), (unsigned)batch);
+  PTO_REQUIRE(grid.y < 65536 && grid.z < 65536, "pack: grid too large");
+  if (sizeof(S) == 8 || sizeof(TO) == 8 || sizeof(TI) == 8)
+    hipLaunchKernelGGL((pack_kernel_f64<TI, TO, S>), grid, dim3(256), 0, stream, in, rows, cols, ld_in, s_in, scale,
+                       out_s, ld_s, s_s, out_t, ld_t, s_t, ones ? 1 : 0);
+  else
+    hipLaunchKernelGGL((pack_kernel<TI, TO, S>), grid, dim3(256), 0, stream, in, rows, cols, ld_in, s_in, scale,
+                       out_s, ld_s, s_s, out_t, ld_t, s_t, ones ? 1 : 0);
+  PTO_LAUNCHED("pack");
+  return 0;
+}
+
+// Zero columns [c0, ld) of every row of a batched [rows][ld] buffer.
+template <typename T>
+__global__ void zero_cols_kernel(T* __restrict__ buf, int64_t rows, int64_t ld, int64_t c0, int64_t sb) {
+  const int b = blockIdx.y;
+  const int64_t w = ld - c0, total = rows * w;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = e / w, c = c0 + (e - r * w);
+    buf[(int64_t)b * sb + r * ld + c] = T(0);
+  }
+}
+
+template <typename T>
+int launch_zero_cols(T* buf, int64_t rows, int64_t ld, int64_t c0, int64_t sb, int batch, hipStream_t stream) {
+  if (c0 >= ld || rows == 0 || batch == 0) return 0;
+  int64_t total = rows * (ld - c0);
+  unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 1024);
+  hipLaunchKernelGGL(zero_cols_kernel<T>, dim3(blocks, batch), dim3(256), 0, stream, buf, rows, ld, c0, sb);
+  PTO_LAUNCHED("zero_cols");
+  return 0;
+}
+
+template <typename T>
+__global__ void fill_kernel(T* __restrict__ p, int64_t n, T v) {
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x)
+    p[e] = v;
+}
+
+template <typename T>
+int launch_fill(T* p, int64_t n, T v, hipStream_t stream) {
+  if (n == 0) return 0;
+  unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 2048);
+  hipLaunchKernelGGL(fill_kernel<T>, dim3(blocks), dim3(256), 0, stream, p, n, v);
+  PTO_LAUNCHED("fill");
+  return 0;
+}
+
+}  // namespace pto

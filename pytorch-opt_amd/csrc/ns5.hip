@@ -1,0 +1,230 @@
+// Quintic Newton–Schulz orthogonalization on gfx950.
+//
+// Replaces _NATIVE.newton_schulz_orthogonalize
+// (pytorch_opt/ops/__init__.py:67-71, csrc/pytorch_opt_ops.cpp:65-81) with
+// the same semantics as pytorch_opt/ops/reference.py:71-97:
+//   X = G (work precision); if rows > cols, X = Xᵀ;  X /= (‖X‖_F + eps);
+//   repeat `steps` times:  A = X·Xᵀ;  B = b·A + c·A·A;  X = a·X + B·X;
+//   undo the transpose; cast back.
+//
+// Per iteration three MFMA launches, each with a fused epilogue:
+//   1. A = X·Xᵀ              symmetric: upper tiles only, mirrored store
+//   2. B = b·A + c·(A·A)     symmetric: upper tiles only, mirrored store
+//   3. X' = a·X + B·X        full; writes X' and X'ᵀ (Xᵀ is the K-major
+//                            operand the next B·X needs)
+// All three are "NT" products over K-contiguous rows. bf16 inputs keep
+// X, A, B in bf16 between launches with fp32 accumulation; fp32 and fp64
+// inputs stay in their own precision throughout.
+#include <algorithm>
+
+#include "aux_kernels.h"
+#include "gemm_nt.h"
+
+namespace pto {
+namespace {
+
+// 1 / (sqrt(sum of partial squares) + eps), one thread per matrix.
+template <typename A>
+__global__ void ns_scale_kernel(const double* __restrict__ partial, int nblk, double eps, A* __restrict__ scale,
+                                int batch) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  double s = 0.0;
+  for (int i = 0; i < nblk; ++i) s += partial[(int64_t)b * nblk + i];
+  A nrm = static_cast<A>(sqrt(s));
+  scale[b] = A(1) / (nrm + static_cast<A>(eps));
+}
+
+// B = b·A + c·v  (A is symmetric, so the mirror takes the same value)
+template <typename T, typename A>
+struct EpiNsSq {
+  typedef A S;
+  const T* Asrc;
+  T* dst;
+  int64_t ld, sd;
+  A bc, cc;
+  bool vec;
+  __device__ __forceinline__ bool has_t() const { return false; }
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, S* vo) const {
+    const int64_t o = (int64_t)b * sd + (int64_t)i * ld + j0;
+    S a[8];
+    ld8<T, S>(Asrc + o, a, kbeg, n, vec);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vo[k] = bc * a[k] + cc * v[k];
+    st8<T, S>(dst + o, vo, kbeg, n, vec);
+  }
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n) const {
+    st8<T, S>(dst + (int64_t)b * sd + (int64_t)j * ld + i0, v, 0, n, vec);
+  }
+  __device__ __forceinline__ void finish(int) const {}
+};
+
+// X' = a·X + v, stored to dst (row-major) and/or dstT (transposed copy).
+template <typename T, typename A>
+struct EpiNsUpdate {
+  typedef A S;
+  const T* xsrc;
+  int64_t ld_x, s_x;
+  T* dst;
+  int64_t ld_d, s_d;
+  T* dstT;
+  int64_t ld_t, s_t;
+  A ac;
+  bool vec_x, vec_d, vec_t;
+  __device__ __forceinline__ bool has_t() const { return dstT != nullptr; }
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, S* vo) const {
+    S x[8];
+    ld8<T, S>(xsrc + (int64_t)b * s_x + (int64_t)i * ld_x + j0, x, kbeg, n, vec_x);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vo[k] = ac * x[k] + v[k];
+    if (dst) st8<T, S>(dst + (int64_t)b * s_d + (int64_t)i * ld_d + j0, vo, kbeg, n, vec_d);
+  }
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n) const {
+    st8<T, S>(dstT + (int64_t)b * s_t + (int64_t)j * ld_t + i0, v, 0, n, vec_t);
+  }
+  __device__ __forceinline__ void finish(int) const {}
+};
+
+template <typename T>
+struct NsLayout {
+  int64_t m, n, ldm, ldn;
+  bool transposed;
+};
+
+template <typename T>
+size_t ns5_ws_bytes_t(int64_t batch, int64_t rows, int64_t cols) {
+  int64_t m = std::min(rows, cols), n = std::max(rows, cols);
+  int64_t ldm = round_up(m, kPadK), ldn = round_up(n, kPadK);
+  size_t e = sizeof(T);
+  size_t bytes = 0;
+  auto add = [&](size_t b) { bytes = round_up(bytes, 256) + b; };
+  typedef typename AccOf<T>::type A;
+  add(sizeof(double) * kRedBlocks * batch);   // partial sums
+  add(sizeof(A) * batch);                      // scales
+  add(e * batch * m * ldm);                    // A
+  add(e * batch * m * ldm);                    // B
+  add(e * batch * m * ldn);                    // X
+  add(e * batch * n * ldm);                    // Xᵀ ping
+  add(e * batch * n * ldm);                    // Xᵀ pong
+  return bytes + 256;
+}
+
+template <typename T>
+int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t steps, double a, double b, double c,
+          double eps, void* ws, size_t ws_bytes, hipStream_t stream) {
+  typedef typename AccOf<T>::type A;
+  const bool transposed = rows > cols;
+  const int64_t m = std::min(rows, cols), n = std::max(rows, cols);
+  const int64_t ldm = round_up(m, kPadK), ldn = round_up(n, kPadK);
+  PTO_REQUIRE(m <= INT32_MAX && n <= INT32_MAX && batch <= 65535, "newton_schulz_orthogonalize: shape too large");
+  if (batch == 0 || rows == 0 || cols == 0) return 0;
+
+  Carver cv(ws, ws_bytes);
+  double* partial = cv.take<double>(kRedBlocks * batch);
+  A* scale = cv.take<A>(batch);
+  T* Ab = cv.take<T>(batch * m * ldm);
+  T* Bb = cv.take<T>(batch * m * ldm);
+  T* Xb = cv.take<T>(batch * m * ldn);
+  T* XT[2] = {cv.take<T>(batch * n * ldm), cv.take<T>(batch * n * ldm)};
+  PTO_REQUIRE(!cv.overflow, "newton_schulz_orthogonalize: workspace too small");
+  const int nb = (int)batch;
+  const int64_t sG = rows * cols;
+
+  // ‖X‖_F per matrix (deterministic two-stage sum), then 1/(‖X‖+eps).
+  if (launch_sumsq<T>(G, rows, cols, cols, sG, nb, partial, stream)) return -1;
+  hipLaunchKernelGGL(ns_scale_kernel<A>, dim3((nb + 63) / 64), dim3(64), 0, stream, partial, kRedBlocks, eps, scale, nb);
+  PTO_LAUNCHED("ns_scale");
+
+  if (steps == 0) {  // the normalised input, in the input's layout
+    if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, out, cols, sG, nullptr, 0, 0, false, nb, stream)) return -1;
+    return 0;
+  }
+
+  // X0 = s·X in both layouts, pads zeroed.
+  if (!transposed) {
+    if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, Xb, ldn, m * ldn, XT[0], ldm, n * ldm, false, nb, stream))
+      return -1;
+  } else {
+    if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, XT[0], ldm, n * ldm, Xb, ldn, m * ldn, false, nb, stream))
+      return -1;
+  }
+  if (launch_zero_cols<T>(XT[1], n, ldm, m, n * ldm, nb, stream)) return -1;
+  if (launch_zero_cols<T>(Ab, m, ldm, m, m * ldm, nb, stream)) return -1;
+  if (launch_zero_cols<T>(Bb, m, ldm, m, m * ldm, nb, stream)) return -1;
+
+  int cur = 0;  // XT[cur] holds X_tᵀ
+  for (int64_t t = 0; t < steps; ++t) {
+    const bool last = t == steps - 1;
+    // 1. A = X·Xᵀ
+    {
+      GemmArgs g{Xb, ldn, m * ldn, Xb, ldn, m * ldn, (int)m, (int)m, (int)ldn, 0, 0, nullptr};
+      EpiStore<T, A> e{Ab, ldm, m * ldm, vec_ok<T>(Ab, ldm, m * ldm)};
+      if (launch_gemm<T, true>(g, e, nb, stream, "ns5_gram")) return -1;
+    }
+    // 2. B = b·A + c·A·A
+    {
+      GemmArgs g{Ab, ldm, m * ldm, Ab, ldm, m * ldm, (int)m, (int)m, (int)ldm, 0, 0, nullptr};
+      EpiNsSq<T, A> e{Ab, Bb, ldm, m * ldm, static_cast<A>(b), static_cast<A>(c),
+                      vec_ok<T>(Ab, ldm, m * ldm) && vec_ok<T>(Bb, ldm, m * ldm)};
+      if (launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
+    }
+    // 3. X' = a·X + B·X   (B·X as B·(Xᵀ)ᵀ over the stored transpose)
+    {
+      GemmArgs g{Bb, ldm, m * ldm, XT[cur], ldm, n * ldm, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
+      EpiNsUpdate<T, A> e{};
+      e.xsrc = Xb; e.ld_x = ldn; e.s_x = m * ldn; e.ac = static_cast<A>(a);
+      if (!last) {
+        e.dst = Xb; e.ld_d = ldn; e.s_d = m * ldn;
+        e.dstT = XT[cur ^ 1]; e.ld_t = ldm; e.s_t = n * ldm;
+      } else if (!transposed) {
+        e.dst = out; e.ld_d = cols; e.s_d = sG;
+        e.dstT = nullptr;
+      } else {
+        e.dst = nullptr;
+        e.dstT = out; e.ld_t = cols; e.s_t = sG;
+      }
+      e.vec_x = vec_ok<T>(e.xsrc, e.ld_x, e.s_x);
+      e.vec_d = e.dst && vec_ok<T>(e.dst, e.ld_d, e.s_d);
+      e.vec_t = e.dstT && vec_ok<T>(e.dstT, e.ld_t, e.s_t);
+      if (launch_gemm<T, false>(g, e, nb, stream, "ns5_update")) return -1;
+    }
+    cur ^= 1;
+  }
+  return 0;
+}
+
+}  // namespace
+}  // namespace pto
+
+extern "C" {
+
+size_t pto_ns5_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_t cols) {
+  switch (dtype) {
+    case pto::kBF16: return pto::ns5_ws_bytes_t<pto::bf16>(batch, rows, cols);
+    case pto::kF32: return pto::ns5_ws_bytes_t<float>(batch, rows, cols);
+    case pto::kF64: return pto::ns5_ws_bytes_t<double>(batch, rows, cols);
+    default: return 0;
+  }
+}
+
+int pto_ns5(const void* G, void* out, int dtype, int64_t batch, int64_t rows, int64_t cols, int64_t steps, double a,
+            double b, double c, double eps, void* workspace, size_t ws_bytes, void* stream) {
+  PTO_REQUIRE(batch >= 0 && rows >= 0 && cols >= 0 && steps >= 0,
+              "newton_schulz_orthogonalize: negative extent or steps");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case pto::kBF16:
+      return pto::ns5_t<pto::bf16>(static_cast<const pto::bf16*>(G), static_cast<pto::bf16*>(out), batch, rows, cols,
+                                   steps, a, b, c, eps, workspace, ws_bytes, s);
+    case pto::kF32:
+      return pto::ns5_t<float>(static_cast<const float*>(G), static_cast<float*>(out), batch, rows, cols, steps, a, b,
+                               c, eps, workspace, ws_bytes, s);
+    case pto::kF64:
+      return pto::ns5_t<double>(static_cast<const double*>(G), static_cast<double*>(out), batch, rows, cols, steps, a,
+                                b, c, eps, workspace, ws_bytes, s);
+    default:
+      PTO_REQUIRE(false, "newton_schulz_orthogonalize: unsupported dtype code");
+  }
+}
+
+}  // extern "C"

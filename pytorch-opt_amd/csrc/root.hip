@@ -1,0 +1,410 @@
+// Inverse p-th matrix root by the coupled Newton iteration, on gfx950.
+//
+// Replaces the "newton" branch of _NATIVE.inverse_matrix_root
+// (pytorch_opt/ops/__init__.py:58-64, csrc/pytorch_opt_ops.cpp:15-63),
+// following pytorch_opt/ops/reference.py:17-40 and :43-68:
+//   M  = sym(A in root precision) + damping·I
+//   z  = (1 + p) / (2·max(‖M‖_F, tiny));  X = z^(1/p)·I;  Mk = z·M
+//   loop up to max_iter:
+//     Mi = (1 + 1/p)·I − Mk/p;  X = X·Mi;  Mk = Mi^p·Mk;  err = max|Mk − I|
+//     stop keeping the previous X if err > 1.2·previous err; stop if err < tol
+//   return sym(X) in the input dtype
+// `err` is one maximum over the whole batch, as in the reference.
+//
+// Symmetric formulation. In exact arithmetic Mk, Mi and every power of Mi
+// are symmetric (all are polynomials in M). Here they are symmetric by
+// construction: Mi^p and Mi^p·Mk are computed on upper tiles only and
+// mirrored. That halves the MFMA work of three of the four products and is
+// also what keeps fp32 stable: with full products (the reference's form)
+// but symmetrised powers, Mk's antisymmetric rounding part is never
+// corrected and X drifts; with Mk kept symmetric the iteration converges
+// like the reference's (same err floor) with a smaller final residual.
+// X·Mi stays a full product (X is not symmetrised until the end).
+//
+// Device-side control: every kernel of an iteration checks a device flag
+// and exits at once after the stop decision, and a one-thread kernel makes
+// that decision from err. The host enqueues iterations in chunks and reads
+// the flag once per chunk instead of once per iteration. X ping-pongs
+// between two buffers, so the "previous iterate" is still intact when the
+// divergence guard fires.
+#include <algorithm>
+#include <limits>
+
+#include "aux_kernels.h"
+#include "gemm_nt.h"
+
+namespace pto {
+namespace {
+
+template <typename R>
+struct RootState {
+  int stopped;
+  int result;  // index k of the iterate X_k to return
+  int iters;   // loop iterations executed
+  int pad;
+  R prev_err;
+};
+
+template <typename R>
+struct Bits;
+template <>
+struct Bits<float> {
+  typedef unsigned int U;
+  __device__ static U of(float v) { return __float_as_uint(v); }
+};
+template <>
+struct Bits<double> {
+  typedef unsigned long long U;
+  __device__ static U of(double v) { return (U)__double_as_longlong(v); }
+};
+
+// M = sym(A) + damping·I in precision R, [n][ld] with zeroed pads.
+template <typename TI, typename R>
+__global__ void __launch_bounds__(256) root_sym_kernel(const TI* __restrict__ A, int64_t n, int64_t sA, R damping,
+                                                       R* __restrict__ M, int64_t ld, int64_t sM) {
+  __shared__ R t1[32][33], t2[32][33];
+  const int b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const TI* Ab = A + (int64_t)b * sA;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+  for (int rr = ty; rr < 32; rr += 8) {
+    int64_t r = r0 + rr, c = c0 + tx;
+    t1[rr][tx] = (r < n && c < n) ? convert<R>(Ab[r * n + c]) : R(0);
+    int64_t r2 = c0 + rr, c2 = r0 + tx;  // the mirrored tile A[c0.., r0..]
+    t2[rr][tx] = (r2 < n && c2 < n) ? convert<R>(Ab[r2 * n + c2]) : R(0);
+  }
+  __syncthreads();
+  R* Mb = M + (int64_t)b * sM;
+  for (int rr = ty; rr < 32; rr += 8) {
+    int64_t r = r0 + rr, c = c0 + tx;
+    if (r >= n || c >= ld) continue;
+    R v = R(0);
+    if (c < n) {
+      v = R(0.5) * (t1[rr][tx] + t2[tx][rr]);
+      if (r == c && damping != R(0)) v = v + damping;
+    }
+    Mb[r * ld + c] = v;
+  }
+}
+
+// z = (1+p)/(2·max(‖M‖_F, tiny)), xs = z^(1/p), per matrix.
+template <typename R>
+__global__ void root_scale_kernel(const double* __restrict__ partial, int nblk, int p, R tiny, R* __restrict__ z,
+                                  R* __restrict__ xs, int batch) {
+  int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= batch) return;
+  double s = 0.0;
+  for (int i = 0; i < nblk; ++i) s += partial[(int64_t)b * nblk + i];
+  R fro = static_cast<R>(sqrt(s));
+  if (fro < tiny) fro = tiny;  // clamp_min; NaN compares false and passes through
+  R zz = static_cast<R>(1.0 + p) / (R(2) * fro);
+  z[b] = zz;
+  xs[b] = pow(zz, static_cast<R>(1.0 / p));
+}
+
+// X0 = xs·I, Mk0 = z·M, Mi0 = c1·I + alpha·Mk0.
+template <typename R>
+__global__ void root_init_kernel(const R* __restrict__ M, int64_t n, int64_t ld, int64_t sb, const R* __restrict__ z,
+                                 const R* __restrict__ xs, R c1, R alpha, R* __restrict__ X0, R* __restrict__ Mk,
+                                 R* __restrict__ Mi) {
+  const int b = blockIdx.y;
+  const int64_t total = n * ld;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    int64_t r = e / ld, c = e - r * ld;
+    int64_t o = (int64_t)b * sb + e;
+    R x = R(0), mk = R(0), mi = R(0);
+    if (c < n) {
+      mk = M[o] * z[b];
+      mi = alpha * mk;
+      if (r == c) {
+        mi = c1 + mi;
+        x = xs[b];
+      }
+    }
+    X0[o] = x;
+    Mk[o] = mk;
+    Mi[o] = mi;
+  }
+}
+
+// Epilogue of Mk' = Mi^p·Mk (upper tiles + mirror): writes Mk' and the next
+// Mi and folds max|Mk' − I| into err (bitwise max of non-negative values,
+// which keeps NaN).
+template <typename R>
+struct EpiMk {
+  typedef R S;
+  R* Mk;
+  R* Mi;
+  int64_t ld, sb;
+  R c1, alpha;
+  typename Bits<R>::U* err;
+  typename Bits<R>::U mx;
+  bool vec;
+  __device__ __forceinline__ bool has_t() const { return false; }
+  // Row `row`, columns c0+k for k in [kbeg, n).
+  __device__ __forceinline__ void run(int b, int row, int c0, const R* v, int kbeg, int n) {
+    const int64_t o = (int64_t)b * sb + (int64_t)row * ld + c0;
+    R mi[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      R d = v[k];
+      mi[k] = alpha * v[k];
+      if (row == c0 + k) {
+        mi[k] = c1 + mi[k];
+        d = v[k] - R(1);
+      }
+      if (k >= kbeg && k < n) {
+        typename Bits<R>::U u = Bits<R>::of(fabs(d));
+        mx = u > mx ? u : mx;
+      }
+    }
+    st8<R, R>(Mk + o, v, kbeg, n, vec);
+    st8<R, R>(Mi + o, mi, kbeg, n, vec);
+  }
+  __device__ __forceinline__ void put(int b, int i, int j0, const R* v, int kbeg, int n, R* vo) {
+    run(b, i, j0, v, kbeg, n);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vo[k] = v[k];
+  }
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const R* v, int n) { run(b, j, i0, v, 0, n); }
+  __device__ __forceinline__ void finish(int) {
+    for (int off = 32; off > 0; off >>= 1) {
+      typename Bits<R>::U o = __shfl_xor(mx, off, 64);
+      mx = o > mx ? o : mx;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(err, mx);
+  }
+};
+
+template <typename R>
+__global__ void root_decide_kernel(RootState<R>* st, const R* __restrict__ err, int it, R tol) {
+  if (threadIdx.x != 0 || st->stopped) return;
+  R e = err[it];
+  st->iters = it + 1;
+  if (it > 0 && e > st->prev_err * R(1.2)) {  // diverging: keep the last good iterate
+    st->stopped = 1;
+    st->result = it;
+  } else {
+    st->prev_err = e;
+    st->result = it + 1;
+    if (e < tol) st->stopped = 1;
+  }
+}
+
+// out = sym(X_result) cast to the input dtype.
+template <typename R, typename TO>
+__global__ void __launch_bounds__(256) root_final_kernel(const R* __restrict__ X0, const R* __restrict__ X1,
+                                                         const RootState<R>* st, int64_t n, int64_t ld, int64_t sb,
+                                                         TO* __restrict__ out) {
+  __shared__ R t1[32][33], t2[32][33];
+  const R* X = (st->result & 1) ? X1 : X0;
+  const int b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+  const R* Xb = X + (int64_t)b * sb;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int rr = ty; rr < 32; rr += 8) {
+    int64_t r = r0 + rr, c = c0 + tx;
+    t1[rr][tx] = (r < n && c < n) ? Xb[r * ld + c] : R(0);
+    int64_t r2 = c0 + rr, c2 = r0 + tx;
+    t2[rr][tx] = (r2 < n && c2 < n) ? Xb[r2 * ld + c2] : R(0);
+  }
+  __syncthreads();
+  TO* ob = out + (int64_t)b * n * n;
+  for (int rr = ty; rr < 32; rr += 8) {
+    int64_t r = r0 + rr, c = c0 + tx;
+    if (r < n && c < n) ob[r * n + c] = convert<TO>(R(0.5) * (t1[rr][tx] + t2[tx][rr]));
+  }
+}
+
+constexpr int kRootBufs = 10;
+
+template <typename R>
+size_t root_ws_bytes_t(int64_t batch, int64_t n, int64_t max_iter) {
+  int64_t ld = round_up(n, kPadK);
+  size_t bytes = 0;
+  auto add = [&](size_t b) { bytes = round_up(bytes, 256) + b; };
+  add(sizeof(double) * kRedBlocks * batch);
+  add(sizeof(R) * batch);
+  add(sizeof(R) * batch);
+  add(sizeof(R) * std::max<int64_t>(max_iter, 1));
+  add(sizeof(RootState<R>));
+  for (int i = 0; i < kRootBufs; ++i) add(sizeof(R) * batch * n * ld);
+  return bytes + 256;
+}
+
+template <typename TI, typename R>
+int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double damping, int64_t max_iter, double tol,
+           void* ws, size_t ws_bytes, int64_t* iters_out, hipStream_t stream) {
+  typedef typename Bits<R>::U U;
+  PTO_REQUIRE(p >= 1, "inverse_matrix_root: p must be a positive integer");
+  PTO_REQUIRE(n <= INT32_MAX && batch <= 65535 && max_iter <= INT32_MAX, "inverse_matrix_root: shape too large");
+  if (iters_out) *iters_out = 0;
+  if (batch == 0 || n == 0) return 0;
+  const int64_t ld = round_up(n, kPadK), sb = n * ld;
+  const int nb = (int)batch;
+  Carver cv(ws, ws_bytes);
+  double* partial = cv.take<double>(kRedBlocks * batch);
+  R* z = cv.take<R>(batch);
+  R* xs = cv.take<R>(batch);
+  R* err = cv.take<R>(std::max<int64_t>(max_iter, 1));
+  RootState<R>* st = cv.take<RootState<R>>(1);
+  R* buf[kRootBufs];
+  for (int i = 0; i < kRootBufs; ++i) buf[i] = cv.take<R>(batch * sb);
+  PTO_REQUIRE(!cv.overflow, "inverse_matrix_root: workspace too small");
+  R* M = buf[0];
+  R* X[2] = {buf[1], buf[2]};
+  R* Mi[2] = {buf[3], buf[4]};
+  R* Mk[2] = {buf[5], buf[6]};
+  R* tmp[3] = {buf[7], buf[8], buf[9]};
+
+  const R c1 = static_cast<R>(1.0 + 1.0 / (double)p);
+  const R alpha = static_cast<R>(-1.0 / (double)p);
+  {
+    dim3 grid((unsigned)((ld + 31) / 32), (unsigned)((n + 31) / 32), (unsigned)nb);
+    hipLaunchKernelGGL((root_sym_kernel<TI, R>), grid, dim3(256), 0, stream, A, n, n * n, static_cast<R>(damping), M,
+                       ld, sb);
+    PTO_LAUNCHED("root_sym");
+  }
+  if (launch_sumsq<R>(M, n, n, ld, sb, nb, partial, stream)) return -1;
+  hipLaunchKernelGGL(root_scale_kernel<R>, dim3((nb + 63) / 64), dim3(64), 0, stream, partial, kRedBlocks, (int)p,
+                     std::numeric_limits<R>::min(), z, xs, nb);
+  PTO_LAUNCHED("root_scale");
+  {
+    unsigned blocks = (unsigned)std::min<int64_t>((sb + 255) / 256, 2048);
+    hipLaunchKernelGGL(root_init_kernel<R>, dim3(blocks, nb), dim3(256), 0, stream, M, n, ld, sb, z, xs, c1, alpha,
+                       X[0], Mk[0], Mi[0]);
+    PTO_LAUNCHED("root_init");
+  }
+  // Pads of the buffers written only by MFMA epilogues must read as zero.
+  for (R* q : {X[1], Mi[1], Mk[1], tmp[0], tmp[1], tmp[2]})
+    if (launch_zero_cols<R>(q, n, ld, n, sb, nb, stream)) return -1;
+  if (launch_fill<R>(err, std::max<int64_t>(max_iter, 1), R(0), stream)) return -1;
+  if (launch_fill<int>(reinterpret_cast<int*>(st), sizeof(RootState<R>) / sizeof(int), 0, stream)) return -1;
+
+  const int* guard = &st->stopped;
+  // dst = P·Q for symmetric Q (Q's rows are its columns); upper = the
+  // product is symmetric too, computed on upper tiles and mirrored.
+  auto product = [&](const R* P, const R* Q, R* dst, bool upper, const char* name) -> int {
+    GemmArgs g{P, ld, sb, Q, ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard};
+    EpiStore<R, R> e{dst, ld, sb, vec_ok<R>(dst, ld, sb)};
+    if (upper) return launch_gemm<R, true>(g, e, nb, stream, name);
+    return launch_gemm<R, false>(g, e, nb, stream, name);
+  };
+
+  auto iteration = [&](int it) -> int {
+    const int cur = it & 1, nxt = cur ^ 1;
+    // X_{it+1} = X_it · Mi
+    if (product(X[cur], Mi[cur], X[nxt], false, "root_xmi")) return -1;
+    // S = Mi^p (torch.linalg.matrix_power order: direct for p <= 3, else
+    // binary powering from the least significant bit)
+    const R* S = nullptr;
+    if (p == 1) {
+      S = Mi[cur];
+    } else if (p == 2) {
+      if (product(Mi[cur], Mi[cur], tmp[0], true, "root_pow")) return -1;
+      S = tmp[0];
+    } else if (p == 3) {
+      if (product(Mi[cur], Mi[cur], tmp[0], true, "root_pow")) return -1;
+      if (product(tmp[0], Mi[cur], tmp[1], true, "root_pow")) return -1;
+      S = tmp[1];
+    } else {
+      const R* zp = nullptr;   // current power Mi^(2^k)
+      const R* res = nullptr;  // accumulated result
+      int64_t k = p;
+      auto free_tmp = [&]() -> R* {
+        for (R* t : tmp)
+          if (t != zp && t != res) return t;
+        return nullptr;
+      };
+      while (k > 0) {
+        const int64_t bit = k & 1;
+        k >>= 1;
+        if (zp == nullptr) {
+          zp = Mi[cur];
+        } else {
+          R* d = free_tmp();
+          if (product(zp, zp, d, true, "root_pow")) return -1;
+          zp = d;
+        }
+        if (bit) {
+          if (res == nullptr) {
+            res = zp;
+          } else {
+            R* d = free_tmp();
+            if (product(res, zp, d, true, "root_pow")) return -1;
+            res = d;
+          }
+        }
+      }
+      S = res;
+    }
+    // Mk_{it+1} = S · Mk_it, with the fused next-Mi / error epilogue.
+    {
+      GemmArgs g{S, ld, sb, Mk[cur], ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard};
+      EpiMk<R> e{Mk[nxt], Mi[nxt], ld, sb, c1, alpha, reinterpret_cast<U*>(err + it), U(0),
+                    vec_ok<R>(Mk[nxt], ld, sb) && vec_ok<R>(Mi[nxt], ld, sb)};
+      if (launch_gemm<R, true>(g, e, nb, stream, "root_mk")) return -1;
+    }
+    hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(64), 0, stream, st, err, it, static_cast<R>(tol));
+    PTO_LAUNCHED("root_decide");
+    return 0;
+  };
+
+  RootState<R> host{};
+  int64_t it = 0;
+  int64_t chunk = 2;
+  while (it < max_iter) {
+    const int64_t end = std::min<int64_t>(max_iter, it + chunk);
+    for (; it < end; ++it)
+      if (iteration((int)it)) return -1;
+    PTO_HIP(hipMemcpyAsync(&host, st, sizeof(host), hipMemcpyDeviceToHost, stream));
+    PTO_HIP(hipStreamSynchronize(stream));
+    if (host.stopped) break;
+    chunk = std::min<int64_t>(chunk * 2, 16);
+  }
+  {
+    dim3 grid((unsigned)((n + 31) / 32), (unsigned)((n + 31) / 32), (unsigned)nb);
+    hipLaunchKernelGGL((root_final_kernel<R, TI>), grid, dim3(256), 0, stream, X[0], X[1], st, n, ld, sb, out);
+    PTO_LAUNCHED("root_final");
+  }
+  if (iters_out) *iters_out = host.iters;
+  return 0;
+}
+
+template <typename TI>
+int root_dispatch(const TI* A, TI* out, int root_f64, int64_t batch, int64_t n, int64_t p, double damping,
+                  int64_t max_iter, double tol, void* ws, size_t ws_bytes, int64_t* iters_out, hipStream_t s) {
+  if (root_f64) return root_t<TI, double>(A, out, batch, n, p, damping, max_iter, tol, ws, ws_bytes, iters_out, s);
+  return root_t<TI, float>(A, out, batch, n, p, damping, max_iter, tol, ws, ws_bytes, iters_out, s);
+}
+
+}  // namespace
+}  // namespace pto
+
+extern "C" {
+
+size_t pto_inverse_root_workspace_bytes(int root_f64, int64_t batch, int64_t n, int64_t max_iter) {
+  return root_f64 ? pto::root_ws_bytes_t<double>(batch, n, max_iter) : pto::root_ws_bytes_t<float>(batch, n, max_iter);
+}
+
+int pto_inverse_root(const void* A, void* out, int dtype, int root_f64, int64_t batch, int64_t n, int64_t p,
+                     double damping, int64_t max_iter, double tol, void* workspace, size_t ws_bytes,
+                     int64_t* iters_out, void* stream) {
+  PTO_REQUIRE(batch >= 0 && n >= 0 && max_iter >= 0, "inverse_matrix_root: negative extent or max_iter");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case pto::kF32:
+      return pto::root_dispatch<float>(static_cast<const float*>(A), static_cast<float*>(out), root_f64, batch, n, p,
+                                       damping, max_iter, tol, workspace, ws_bytes, iters_out, s);
+    case pto::kF64:
+      return pto::root_dispatch<double>(static_cast<const double*>(A), static_cast<double*>(out), root_f64, batch, n,
+                                        p, damping, max_iter, tol, workspace, ws_bytes, iters_out, s);
+    case pto::kBF16:
+      return pto::root_dispatch<pto::bf16>(static_cast<const pto::bf16*>(A), static_cast<pto::bf16*>(out), root_f64,
+                                           batch, n, p, damping, max_iter, tol, workspace, ws_bytes, iters_out, s);
+    default:
+      PTO_REQUIRE(false, "inverse_matrix_root: unsupported dtype code");
+  }
+}
+
+}  // extern "C"

@@ -1,0 +1,111 @@
+"""pytorch_opt.ops — backend-dispatched numerics for the matrix optimizers.
+
+Backends (the same switch as the reference's pytorch_opt/ops/__init__.py:16-88):
+  "reference"  pure torch (pytorch_opt.ops.reference), any device;
+  "native"     the gfx950 HIP library (libpytorch_opt_hip.so) for GPU
+               tensors; CPU tensors take the pure-torch maths, as the
+               reference's compiled backend served CPU tensors through ATen;
+  "auto"       native once loaded, reference otherwise (the default).
+
+``load_native()`` loads the prebuilt library; like the reference it never
+raises (it warns and returns False). ``PYTORCH_OPT_NATIVE=1`` at import
+calls it. Op signatures and defaults are the reference's
+(pytorch_opt/ops/__init__.py:58-84); ``gram_update_`` is additive.
+"""
+
+from __future__ import annotations
+
+import os
+import warnings
+
+import torch
+
+from . import reference
+from .reference import OpsArgumentError
+
+_VALID_BACKENDS = ("auto", "native", "reference")
+_BACKEND = "auto"
+_NATIVE = None  # pytorch_opt.ops._hip.HipBackend once loaded
+
+
+def get_backend() -> str:
+    return _BACKEND
+
+
+def native_available() -> bool:
+    return _NATIVE is not None
+
+
+def set_backend(name: str) -> None:
+    """Select the backend (reference: pytorch_opt/ops/__init__.py:29-35)."""
+    global _BACKEND
+    if name not in _VALID_BACKENDS:
+        raise ValueError(f"backend must be one of {_VALID_BACKENDS}, got {name!r}")
+    if name == "native" and _NATIVE is None:
+        raise RuntimeError("native backend not loaded; call pytorch_opt.ops.load_native() first")
+    _BACKEND = name
+
+
+def load_native(verbose: bool = False) -> bool:
+    """Load the HIP library. True on success; never raises (warns instead)."""
+    global _NATIVE
+    if _NATIVE is not None:
+        return True
+    try:
+        from . import native_build
+
+        _NATIVE = native_build.load(verbose=verbose)
+        return True
+    except Exception as exc:  # keep the package usable without the library
+        warnings.warn(f"pytorch-opt: native backend unavailable ({type(exc).__name__}: {exc}); "
+                      f"using reference implementations", RuntimeWarning, stacklevel=2)
+        return False
+
+
+def _use_native() -> bool:
+    return _BACKEND == "native" or (_BACKEND == "auto" and _NATIVE is not None)
+
+
+def inverse_matrix_root(A, p, damping=0.0, method="auto", root_dtype=torch.float64,
+                        max_iter=100, tol=1e-10):
+    if _use_native():
+        return _NATIVE.inverse_matrix_root(A, int(p), float(damping), str(method),
+                                           root_dtype == torch.float64, int(max_iter), float(tol))
+    return reference.inverse_matrix_root(A, p, damping=damping, method=method,
+                                         root_dtype=root_dtype, max_iter=max_iter, tol=tol)
+
+
+def newton_schulz_orthogonalize(G, steps=5, coeffs=(3.4445, -4.7750, 2.0315), eps=1e-7):
+    if _use_native():
+        a, b, c = coeffs
+        return _NATIVE.newton_schulz_orthogonalize(G, int(steps), float(a), float(b), float(c), float(eps))
+    return reference.newton_schulz_orthogonalize(G, steps=steps, coeffs=coeffs, eps=eps)
+
+
+def kron_factor_update_(L, R, G, beta2=1.0):
+    if _use_native():
+        _NATIVE.kron_factor_update_(L, R, G, float(beta2))
+        return L, R
+    return reference.kron_factor_update_(L, R, G, beta2=beta2)
+
+
+def precond_apply_two_sided(L_root, G, R_root):
+    if _use_native():
+        return _NATIVE.precond_apply_two_sided(L_root, G, R_root)
+    return reference.precond_apply_two_sided(L_root, G, R_root)
+
+
+def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
+    """F ← beta·F + alpha·X̃ᵀX̃ in place, X̃ = [X, 1] if append_ones (beta=0 overwrites)."""
+    if _use_native():
+        _NATIVE.gram_update_(F, X, float(beta), float(alpha), bool(append_ones))
+        return F
+    return reference.gram_update_(F, X, beta=beta, alpha=alpha, append_ones=append_ones)
+
+
+__all__ = ["get_backend", "set_backend", "native_available", "load_native", "inverse_matrix_root",
+           "newton_schulz_orthogonalize", "kron_factor_update_", "precond_apply_two_sided",
+           "gram_update_", "OpsArgumentError", "reference"]
+
+if os.environ.get("PYTORCH_OPT_NATIVE") == "1":
+    load_native()

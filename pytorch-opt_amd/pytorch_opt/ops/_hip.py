@@ -1,0 +1,247 @@
+"""ctypes adapter from torch tensors to the C ABI of libpytorch_opt_hip.so.
+
+``HipBackend`` is the object the dispatch layer stores in ``ops._NATIVE``.
+Its methods take the exact positional forms the dispatch calls
+(pytorch_opt/ops/__init__.py:61-62,70,76,83 in the reference) and turn
+tensors into device pointers, extents, a dtype code, a torch-allocated
+workspace and the current HIP stream. GPU tensors always run the HIP
+kernels; a failing call raises RuntimeError with the library's message and
+never falls back. CPU tensors take the pure-torch maths, as the reference's
+compiled backend served CPU tensors through ATen.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import reference
+from .reference import OpsArgumentError, ROOT_METHODS
+
+_DTYPE_CODE = {torch.float32: 0, torch.float64: 1, torch.bfloat16: 2}
+
+_c_size = ctypes.c_size_t
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_dbl = ctypes.c_double
+_c_ptr = ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/pytorch_opt_hip.h
+SIGNATURES = {
+    "pto_last_error": (ctypes.c_char_p, []),
+    "pto_version": (_c_int, []),
+    "pto_runtime_version": (_c_int, []),
+    "pto_ns5_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "pto_ns5": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_dbl, _c_dbl, _c_dbl,
+                         _c_dbl, _c_ptr, _c_size, _c_ptr]),
+    "pto_kron_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "pto_kron_factor_update": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr,
+                                        _c_size, _c_ptr]),
+    "pto_gram_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_int]),
+    "pto_gram_update": (_c_int, [_c_ptr, _c_int, _c_ptr, _c_int, _c_i64, _c_i64, _c_int, _c_dbl, _c_dbl,
+                                 _c_ptr, _c_size, _c_ptr]),
+    "pto_inverse_root_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "pto_inverse_root": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_dbl, _c_i64,
+                                  _c_dbl, _c_ptr, _c_size, ctypes.POINTER(_c_i64), _c_ptr]),
+    "pto_precond_apply_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "pto_precond_apply": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_size,
+                                   _c_ptr]),
+    "pto_prof_enable": (_c_int, [_c_int]),
+    "pto_prof_reset": (_c_int, []),
+    "pto_prof_query": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_c_dbl), ctypes.POINTER(_c_i64)]),
+}
+
+
+def _ptr(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _overlaps(a: torch.Tensor, b: torch.Tensor) -> bool:
+    if a.device != b.device or a.numel() == 0 or b.numel() == 0:
+        return False
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    a1 = a0 + a.numel() * a.element_size()
+    b1 = b0 + b.numel() * b.element_size()
+    return a0 < b1 and b0 < a1
+
+
+class HipBackend:
+    """The compiled backend object: same call forms as the reference's _NATIVE."""
+
+    def __init__(self, path: str):
+        self.path = path
+        self._lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(self._lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        self.version = self._lib.pto_version()
+
+    # ------------------------------------------------------------ plumbing
+    def _check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            msg = self._lib.pto_last_error().decode(errors="replace")
+            raise RuntimeError(f"{what}: {msg} (status {rc})")
+
+    @staticmethod
+    def _stream(dev: torch.device) -> ctypes.c_void_p:
+        return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+    @staticmethod
+    def _workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+    # ------------------------------------------------------------ ops
+    def newton_schulz_orthogonalize(self, G, steps, a, b, c, eps):
+        if G.dim() < 2:
+            raise OpsArgumentError("newton_schulz_orthogonalize expects a matrix (ndim >= 2)")
+        if not G.is_cuda:
+            return reference.newton_schulz_orthogonalize(G, steps, (a, b, c), eps)
+        if G.dtype not in _DTYPE_CODE:  # e.g. float16: the float32 path, cast back
+            return self.newton_schulz_orthogonalize(G.float(), steps, a, b, c, eps).to(G.dtype)
+        Gc = G.contiguous()
+        rows, cols = Gc.shape[-2], Gc.shape[-1]
+        batch = math.prod(Gc.shape[:-2])
+        out = torch.empty_like(Gc)
+        code = _DTYPE_CODE[Gc.dtype]
+        with torch.cuda.device(Gc.device):
+            nbytes = self._lib.pto_ns5_workspace_bytes(code, batch, rows, cols)
+            ws = self._workspace(nbytes, Gc.device)
+            rc = self._lib.pto_ns5(_ptr(Gc), _ptr(out), code, batch, rows, cols, max(int(steps), 0),
+                                   float(a), float(b), float(c), float(eps), _ptr(ws), nbytes,
+                                   self._stream(Gc.device))
+        self._check(rc, "newton_schulz_orthogonalize")
+        return out
+
+    def kron_factor_update_(self, L, R, G, beta2):
+        if G.dim() != 2:
+            raise OpsArgumentError(f"G must be 2D, got shape {tuple(G.shape)}")
+        if not (G.is_cuda and L.is_cuda and R.is_cuda):
+            reference.kron_factor_update_(L, R, G, beta2)
+            return
+        m, n = G.shape
+        if tuple(L.shape) != (m, m) or tuple(R.shape) != (n, n):
+            raise OpsArgumentError(f"kron_factor_update_: L {tuple(L.shape)} and R {tuple(R.shape)} "
+                                   f"do not match G {tuple(G.shape)}")
+        if L.dtype != R.dtype:
+            raise OpsArgumentError("kron_factor_update_: L and R must share a dtype")
+        work = L.dtype if L.dtype in _DTYPE_CODE else torch.float32
+        Lw = L if (L.dtype == work and L.is_contiguous()) else L.to(work).contiguous()
+        Rw = R if (R.dtype == work and R.is_contiguous()) else R.to(work).contiguous()
+        Gw = G.to(work).contiguous()
+        if _overlaps(Gw, Lw) or _overlaps(Gw, Rw):
+            Gw = Gw.clone()  # the update reads G after writing L/R
+        code = _DTYPE_CODE[work]
+        with torch.cuda.device(Gw.device):
+            nbytes = self._lib.pto_kron_workspace_bytes(code, m, n)
+            ws = self._workspace(nbytes, Gw.device)
+            rc = self._lib.pto_kron_factor_update(_ptr(Lw), _ptr(Rw), _ptr(Gw), code, m, n, float(beta2),
+                                                  _ptr(ws), nbytes, self._stream(Gw.device))
+        self._check(rc, "kron_factor_update_")
+        if Lw is not L:
+            L.copy_(Lw)
+        if Rw is not R:
+            R.copy_(Rw)
+
+    def inverse_matrix_root(self, A, p, damping, method, root_f64, max_iter, tol):
+        return self.inverse_matrix_root_iters(A, p, damping, method, root_f64, max_iter, tol)[0]
+
+    def inverse_matrix_root_iters(self, A, p, damping, method, root_f64, max_iter, tol):
+        """inverse_matrix_root plus the number of Newton iterations run."""
+        if int(p) != p or p < 1:
+            raise OpsArgumentError(f"p must be a positive integer, got {p}")
+        if method not in ROOT_METHODS:
+            raise OpsArgumentError(f"method must be one of {ROOT_METHODS}, got {method!r}")
+        root_dtype = torch.float64 if root_f64 else torch.float32
+        if not A.is_cuda or method == "eigh":
+            # eigendecomposition is not one of the kernels here: torch's eigh
+            return reference.inverse_matrix_root_with_iters(A, p, damping, method, root_dtype, max_iter, tol)
+        if A.dim() < 2 or A.shape[-1] != A.shape[-2]:
+            raise OpsArgumentError(f"inverse_matrix_root expects square matrices, got {tuple(A.shape)}")
+        if A.dtype not in _DTYPE_CODE:
+            out, iters = self.inverse_matrix_root_iters(A.float(), p, damping, method, root_f64, max_iter, tol)
+            return out.to(A.dtype), iters
+        Ac = A.contiguous()
+        n = Ac.shape[-1]
+        batch = math.prod(Ac.shape[:-2])
+        out = torch.empty_like(Ac)
+        code = _DTYPE_CODE[Ac.dtype]
+        iters = _c_i64(0)
+        with torch.cuda.device(Ac.device):
+            nbytes = self._lib.pto_inverse_root_workspace_bytes(int(bool(root_f64)), batch, n, max(int(max_iter), 0))
+            ws = self._workspace(nbytes, Ac.device)
+            rc = self._lib.pto_inverse_root(_ptr(Ac), _ptr(out), code, int(bool(root_f64)), batch, n, int(p),
+                                            float(damping), max(int(max_iter), 0), float(tol), _ptr(ws), nbytes,
+                                            ctypes.byref(iters), self._stream(Ac.device))
+        self._check(rc, "inverse_matrix_root")
+        return out, int(iters.value)
+
+    def precond_apply_two_sided(self, L_root, G, R_root):
+        if not (L_root.is_cuda and G.is_cuda and R_root.is_cuda):
+            return reference.precond_apply_two_sided(L_root, G, R_root)
+        if L_root.dim() < 2 or G.dim() < 2 or R_root.dim() < 2:
+            raise OpsArgumentError("precond_apply_two_sided expects matrices")
+        m, n = G.shape[-2], G.shape[-1]
+        if L_root.shape[-2:] != (m, m) or R_root.shape[-2:] != (n, n):
+            raise OpsArgumentError(f"precond_apply_two_sided: shapes {tuple(L_root.shape)}, {tuple(G.shape)}, "
+                                   f"{tuple(R_root.shape)} do not chain")
+        out_dtype = torch.promote_types(torch.promote_types(L_root.dtype, G.dtype), R_root.dtype)
+        work = out_dtype if out_dtype in _DTYPE_CODE else torch.float32
+        lead = torch.broadcast_shapes(L_root.shape[:-2], G.shape[:-2], R_root.shape[:-2])
+        Lb = L_root.to(work).expand(*lead, m, m).reshape(-1, m, m)
+        Gb = G.to(work).expand(*lead, m, n).reshape(-1, m, n)
+        Rb = R_root.to(work).expand(*lead, n, n).reshape(-1, n, n)
+        out = torch.empty(Gb.shape, dtype=work, device=G.device)
+        code = _DTYPE_CODE[work]
+        with torch.cuda.device(G.device):
+            nbytes = self._lib.pto_precond_apply_workspace_bytes(code, m, n)
+            ws = self._workspace(nbytes, G.device)
+            stream = self._stream(G.device)
+            for i in range(out.shape[0]):
+                Li, Gi, Ri = Lb[i].contiguous(), Gb[i].contiguous(), Rb[i].contiguous()
+                rc = self._lib.pto_precond_apply(_ptr(Li), _ptr(Gi), _ptr(Ri), _ptr(out[i]), code, m, n,
+                                                 _ptr(ws), nbytes, stream)
+                self._check(rc, "precond_apply_two_sided")
+        out = out.reshape(*lead, m, n)
+        return out if out.dtype == out_dtype else out.to(out_dtype)
+
+    def gram_update_(self, F, X, beta, alpha, append_ones):
+        if not (F.is_cuda and X.is_cuda):
+            reference.gram_update_(F, X, beta, alpha, append_ones)
+            return
+        d = X.shape[-1]
+        X2 = X.reshape(-1, d)
+        dd = d + (1 if append_ones else 0)
+        if tuple(F.shape) != (dd, dd):
+            raise OpsArgumentError(f"gram_update_: F {tuple(F.shape)} does not match X̃ width {dd}")
+        f_work = F.dtype if F.dtype in (torch.float32, torch.float64) else torch.float32
+        x_work = X2.dtype if (X2.dtype == torch.bfloat16 and f_work == torch.float32) else f_work
+        Fw = F if (F.dtype == f_work and F.is_contiguous()) else F.to(f_work).contiguous()
+        Xw = X2.to(x_work).contiguous()
+        if _overlaps(Xw, Fw):
+            Xw = Xw.clone()
+        fc, xc = _DTYPE_CODE[f_work], _DTYPE_CODE[x_work]
+        rows = Xw.shape[0]
+        with torch.cuda.device(Fw.device):
+            nbytes = self._lib.pto_gram_workspace_bytes(xc, rows, d, int(bool(append_ones)))
+            ws = self._workspace(nbytes, Fw.device)
+            rc = self._lib.pto_gram_update(_ptr(Fw), fc, _ptr(Xw), xc, rows, d, int(bool(append_ones)),
+                                           float(beta), float(alpha), _ptr(ws), nbytes, self._stream(Fw.device))
+        self._check(rc, "gram_update_")
+        if Fw is not F:
+            F.copy_(Fw)
+
+    # ------------------------------------------------------------ timing
+    def prof_enable(self, on: bool) -> None:
+        self._check(self._lib.pto_prof_enable(int(bool(on))), "prof_enable")
+
+    def prof_reset(self) -> None:
+        self._check(self._lib.pto_prof_reset(), "prof_reset")
+
+    def prof_query(self, name: str):
+        """(total milliseconds, launches) recorded for one kernel class."""
+        ms, n = _c_dbl(0.0), _c_i64(0)
+        self._check(self._lib.pto_prof_query(name.encode(), ctypes.byref(ms), ctypes.byref(n)), "prof_query")
+        return ms.value, n.value

@@ -1,0 +1,336 @@
+"""HIP path vs the CPU oracle (and, at full size, vs the package's pure-torch
+reference on the same GPU), through the C ABI. Tolerances are the ones the
+op contracts state: fp32 NS5 atol 1e-5 (the reference's
+tests/test_ops_native_parity.py:43-48), bf16 NS5 relative Frobenius 2e-2,
+fp32 factor updates relative Frobenius 1e-4, inverse-root residual within
+1e-3 of the reference's."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops_oracle as oo
+from pytorch_opt import ops
+from pytorch_opt.ops import reference as ops_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy() if t.dtype == torch.bfloat16 else t.detach().cpu().numpy()
+
+
+def _relfro(got, want):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-300))
+
+
+# ---------------------------------------------------------------- NS5
+
+def test_ns5_config1_fp32(native_backend):
+    """512x256 fp32 N(0,1) from seed 0 (transposed so rows <= cols), 5 steps."""
+    g = torch.Generator().manual_seed(0)
+    G = torch.randn(512, 256, generator=g)
+    want = oo.ns5(G.numpy())
+    got = ops.newton_schulz_orthogonalize(G.to(DEV))
+    assert got.dtype == torch.float32 and got.shape == G.shape
+    assert np.abs(_np(got) - want).max() < 1e-5
+
+
+@pytest.mark.parametrize("shape", [(8, 5), (5, 8), (4, 6, 9), (100, 37), (3, 70, 130), (64, 64), (1, 1),
+                                   (2, 3, 256, 192)])
+def test_ns5_fp32_shapes(native_backend, shape):
+    G = torch.randn(*shape)
+    want = oo.ns5(G.numpy())
+    got = ops.newton_schulz_orthogonalize(G.to(DEV))
+    assert got.shape == G.shape
+    assert np.abs(_np(got) - want).max() < 1e-5, shape
+
+
+@pytest.mark.parametrize("steps", [0, 1, 2, 10])
+def test_ns5_steps_and_coeffs(native_backend, steps):
+    G = torch.randn(40, 72)
+    coeffs = (3.0, -3.2, 1.2)
+    want = oo.ns5(G.numpy(), steps=steps, coeffs=coeffs, eps=1e-5)
+    got = ops.newton_schulz_orthogonalize(G.to(DEV), steps=steps, coeffs=coeffs, eps=1e-5)
+    assert np.abs(_np(got) - want).max() < 1e-5
+
+
+def test_ns5_fp64_and_fp16(native_backend):
+    G = torch.randn(33, 70, dtype=torch.float64)
+    got = ops.newton_schulz_orthogonalize(G.to(DEV))
+    assert got.dtype == torch.float64
+    assert np.abs(_np(got) - oo.ns5(G.numpy())).max() < 1e-12
+    H = torch.randn(24, 40).half()
+    got = ops.newton_schulz_orthogonalize(H.to(DEV))
+    assert got.dtype == torch.float16
+    assert np.abs(got.float().cpu().numpy() - oo.ns5(H.float().numpy())).max() < 2e-3
+
+
+def test_ns5_empty(native_backend):
+    for shape in [(0, 5), (5, 0), (0, 4, 4)]:
+        got = ops.newton_schulz_orthogonalize(torch.randn(*shape, device=DEV))
+        assert got.shape == shape
+
+
+@pytest.mark.parametrize("shape", [(256, 512), (1024, 1024), (2, 384, 1000), (1000, 384)])
+def test_ns5_bf16_vs_oracle(native_backend, shape):
+    G = (torch.randn(*shape) * 1e-3).bfloat16()
+    want = oo.ns5(G.float().numpy())  # fp32 work, like the reference's upcast
+    got = ops.newton_schulz_orthogonalize(G.to(DEV))
+    assert got.dtype == torch.bfloat16 and got.shape == G.shape
+    assert _relfro(_np(got), want) <= 2e-2
+
+
+def test_ns5_semi_orthogonal_bf16(native_backend):
+    Q, _ = torch.linalg.qr(torch.randn(512, 256, dtype=torch.float64))
+    Q = Q.T.contiguous()  # 256 x 512, rows orthonormal
+    O = ops.newton_schulz_orthogonalize(Q.bfloat16().to(DEV), steps=10).double().cpu()
+    s = float((O * Q).sum() / (Q * Q).sum())
+    assert 0.3 < s < 1.6
+    assert float((O - s * Q).norm() / Q.norm()) < 2e-2
+
+
+def _config2_inputs(n_mats, rows, cols, seed0):
+    """Nesterov momentum (β=0.95) over 3 steps of N(0,1e-3) gradients, bf16."""
+    out = torch.empty(n_mats, rows, cols, dtype=torch.bfloat16, device=DEV)
+    for i in range(n_mats):
+        g = torch.Generator(device=DEV).manual_seed(seed0 + i)
+        buf = torch.zeros(rows, cols, device=DEV)
+        for _ in range(3):
+            gt = 1e-3 * torch.randn(rows, cols, generator=g, device=DEV)
+            buf.mul_(0.95).add_(gt)
+        out[i] = (gt + 0.95 * buf).bfloat16()
+    return out
+
+
+@pytest.mark.parametrize("cols", [4096, 11008])
+def test_ns5_bf16_config2_full_size(native_backend, cols):
+    """Config-2 batch of 32 bf16 matrices: every matrix vs the package's
+    pure-torch fp32 reference on the GPU; one matrix also vs the oracle."""
+    G = _config2_inputs(32, 4096, cols, 1000 if cols == 4096 else 2000)
+    got = ops.newton_schulz_orthogonalize(G)
+    torch.cuda.synchronize()
+    worst = 0.0
+    for i in range(32):
+        want = ops_ref.newton_schulz_orthogonalize(G[i].float())
+        err = float((got[i].float() - want).norm() / want.norm())
+        worst = max(worst, err)
+    assert worst <= 2e-2, worst
+    want0 = oo.ns5(G[0].float().cpu().numpy())
+    assert _relfro(_np(got[0]), want0) <= 2e-2
+
+
+# ---------------------------------------------------------------- kron
+
+@pytest.mark.parametrize("beta2", [1.0, 0.9, 0.95])
+@pytest.mark.parametrize("shape", [(4, 7), (64, 96), (300, 200), (129, 65)])
+def test_kron_vs_oracle(native_backend, beta2, shape):
+    m, n = shape
+    g = torch.Generator().manual_seed(12)
+    G1, G2 = (torch.randn(m, n, generator=g) for _ in range(2))
+    L, R = torch.zeros(m, m, device=DEV), torch.zeros(n, n, device=DEV)
+    Lo, Ro = np.zeros((m, m), np.float32), np.zeros((n, n), np.float32)
+    for G in (G1, G2):
+        ops.kron_factor_update_(L, R, G.to(DEV), beta2=beta2)
+        Lo, Ro = oo.kron_factor_update(Lo, Ro, G.numpy(), beta2)
+    assert _relfro(_np(L), Lo) <= 1e-5 and _relfro(_np(R), Ro) <= 1e-5
+    assert torch.equal(L, L.T) and torch.equal(R, R.T)
+
+
+def test_kron_nonsymmetric_prior_and_fp64(native_backend):
+    m, n = 70, 45
+    L0 = torch.randn(m, m, dtype=torch.float64)
+    R0 = torch.randn(n, n, dtype=torch.float64)
+    G = torch.randn(m, n, dtype=torch.float64)
+    L, R = L0.to(DEV), R0.to(DEV)
+    ops.kron_factor_update_(L, R, G.to(DEV), beta2=0.7)
+    Lo, Ro = oo.kron_factor_update(L0.numpy(), R0.numpy(), G.numpy(), 0.7)
+    assert np.abs(_np(L) - Lo).max() < 1e-12 and np.abs(_np(R) - Ro).max() < 1e-12
+
+
+def test_kron_config3_full_size(native_backend):
+    """fp32 G 4096² ~ N(0,1e-2), β=0.95, priors = Gram matrices of G0."""
+    g = torch.Generator(device=DEV).manual_seed(2)
+    G0 = 1e-2 * torch.randn(4096, 4096, generator=g, device=DEV)
+    G = 1e-2 * torch.randn(4096, 4096, generator=g, device=DEV)
+    L, R = G0 @ G0.T, G0.T @ G0
+    Lr, Rr = L.clone(), R.clone()
+    ops.kron_factor_update_(L, R, G, beta2=0.95)
+    Lw = 0.95 * Lr.double() + 0.05 * (G.double() @ G.double().T)
+    Rw = 0.95 * Rr.double() + 0.05 * (G.double().T @ G.double())
+    assert float((L.double() - Lw).norm() / Lw.norm()) <= 1e-4
+    assert float((R.double() - Rw).norm() / Rw.norm()) <= 1e-4
+
+
+# ---------------------------------------------------------------- gram (K-FAC)
+
+@pytest.mark.parametrize("append_ones", [False, True])
+def test_gram_vs_oracle(native_backend, append_ones):
+    X = torch.randn(3, 50, 70).bfloat16()
+    dd = 70 + int(append_ones)
+    F = torch.zeros(dd, dd, device=DEV)
+    ops.gram_update_(F, X.to(DEV), beta=0.0, alpha=1 / 150, append_ones=append_ones)
+    want = oo.gram_update(None, X.float().numpy(), 0.0, 1 / 150, append_ones)
+    assert _relfro(_np(F), want) <= 1e-6
+    F0 = _np(F).copy()
+    X2 = torch.randn(150, 70).bfloat16()
+    ops.gram_update_(F, X2.to(DEV), beta=0.95, alpha=0.05 / 150, append_ones=append_ones)
+    want = oo.gram_update(F0, X2.float().numpy(), 0.95, 0.05 / 150, append_ones)
+    assert _relfro(_np(F), want) <= 1e-6
+
+
+def test_gram_config3_full_size(native_backend):
+    """bf16 A [16384, 4096] ~ N(0,1) -> fp32 AᵀA/16384 blended into a prior."""
+    g = torch.Generator(device=DEV).manual_seed(3)
+    A = torch.randn(16384, 4096, generator=g, device=DEV).bfloat16()
+    P = torch.randn(4096, 4096, generator=g, device=DEV)
+    prior = P @ P.T / 4096
+    F = prior.clone()
+    ops.gram_update_(F, A, beta=0.95, alpha=0.05 / 16384)
+    Af = A.double()
+    want = 0.95 * prior.double() + 0.05 * (Af.T @ Af) / 16384
+    assert float((F.double() - want).norm() / want.norm()) <= 1e-4
+
+
+# ---------------------------------------------------------------- roots
+
+def _psd(shape, seed=11, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    B = torch.randn(*shape, generator=g).to(dtype)
+    return B @ B.mT + 0.1 * torch.eye(shape[-1], dtype=dtype)
+
+
+@pytest.mark.parametrize("p", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("root_dtype", [torch.float32, torch.float64])
+def test_root_newton_vs_oracle(native_backend, p, root_dtype):
+    A = _psd((6, 6))
+    want, it_o = oo.inverse_root(A.numpy(), p, damping=1e-6, method="newton",
+                                 root_dtype=np.float64 if root_dtype == torch.float64 else np.float32)
+    got, it_h = native_backend.inverse_matrix_root_iters(A.to(DEV), p, 1e-6, "newton",
+                                                         root_dtype == torch.float64, 100, 1e-10)
+    tol = 1e-9 if root_dtype == torch.float64 else 2e-5
+    assert np.abs(_np(got) - want).max() < tol * max(1.0, np.abs(want).max())
+    if root_dtype == torch.float64:
+        assert it_h == it_o
+
+
+def test_root_batched_auto_and_eigh(native_backend):
+    # the reference's test_root_parity (tests/test_ops_native_parity.py:30-40)
+    A = _psd((6, 6))
+    Ab = _psd((3, 5, 5))
+    for p in (1, 2, 4):
+        for method in ("eigh", "newton", "auto"):
+            got = ops.inverse_matrix_root(A.to(DEV), p, damping=1e-6, method=method)
+            want = ops_ref.inverse_matrix_root(A, p, damping=1e-6, method=method if method != "auto" else "eigh")
+            assert torch.allclose(got.cpu(), want, atol=1e-6), (p, method)
+    got = ops.inverse_matrix_root(Ab.to(DEV), 4, damping=1e-6)
+    want = ops_ref.inverse_matrix_root(Ab, 4, damping=1e-6)
+    assert torch.allclose(got.cpu(), want, atol=1e-6)
+
+
+def test_root_divergence_guard_and_max_iter(native_backend):
+    """Indefinite input: the error grows and the guard returns the previous
+    iterate, at the same iteration the oracle stops (fp64, deterministic)."""
+    rng = np.random.default_rng(0)
+    Q, _ = np.linalg.qr(rng.standard_normal((12, 12)))
+    lam = np.concatenate([np.linspace(1, 2, 11), [-3.0]])
+    A = (Q * lam) @ Q.T
+    want, it_o = oo.inverse_root(A, 2, method="newton", root_dtype=np.float64)
+    got, it_h = native_backend.inverse_matrix_root_iters(torch.from_numpy(A).to(DEV), 2, 0.0, "newton", True, 100,
+                                                         1e-10)
+    assert it_h == it_o < 100
+    assert np.abs(_np(got) - want).max() < 1e-9 * max(1.0, np.abs(want).max())
+    for k in (0, 1, 3):
+        want_k, _ = oo.inverse_root(_psd((7, 7)).double().numpy(), 4, method="newton", max_iter=k)
+        got_k, it_k = native_backend.inverse_matrix_root_iters(_psd((7, 7)).double().to(DEV), 4, 0.0, "newton",
+                                                               True, k, 1e-10)
+        assert it_k == k and np.abs(_np(got_k) - want_k).max() < 1e-12
+
+
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_root_config4_residual(native_backend, n):
+    """fp32 SPD Q·diag(λ)·Qᵀ, λ log-uniform in [1e-6, 1], ε = 1e-6, p = 4:
+    HIP residual within 1e-3 of the torch reference's on the same input."""
+    g = torch.Generator().manual_seed(4)
+    Q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+    g5 = torch.Generator().manual_seed(5)
+    lam = 10 ** (-6 * torch.rand(n, generator=g5, dtype=torch.float64))
+    A = ((Q * lam) @ Q.T).float()
+    Ad = A.to(DEV)
+    got, it_h = native_backend.inverse_matrix_root_iters(Ad, 4, 1e-6, "newton", False, 100, 1e-10)
+    want, it_r = ops_ref.inverse_matrix_root_with_iters(Ad, 4, 1e-6, "newton", torch.float32, 100, 1e-10)
+    M = A.double().to(DEV) + 1e-6 * torch.eye(n, dtype=torch.float64, device=DEV)
+
+    def resid(X):
+        X = X.double()
+        X2 = X @ X
+        return float(((X2 @ X2) @ M - torch.eye(n, dtype=torch.float64, device=DEV)).norm() / n ** 0.5)
+
+    r_h, r_r = resid(got), resid(want)
+    print(f"n={n} residual hip={r_h:.3e} ({it_h} it) reference={r_r:.3e} ({it_r} it)")
+    # fp32 at cond 1e6 never meets tol=1e-10: both runs end on noise, so the
+    # bar is one-sided — no worse than the reference's residual + 1e-3.
+    assert r_h <= r_r + 1e-3
+
+
+# ---------------------------------------------------------------- apply
+
+@pytest.mark.parametrize("shape", [(4, 7), (64, 128), (300, 70), (2048, 2048)])
+def test_apply_vs_oracle(native_backend, shape):
+    m, n = shape
+    Lr, G, Rr = torch.randn(m, m), torch.randn(m, n), torch.randn(n, n)
+    got = ops.precond_apply_two_sided(Lr.to(DEV), G.to(DEV), Rr.to(DEV))
+    want = oo.precond_apply(Lr.double().numpy(), G.double().numpy(), Rr.double().numpy())
+    assert _relfro(_np(got), want) <= 1e-5
+
+
+def test_apply_batched_and_promoted(native_backend):
+    Lr = torch.randn(2, 5, 5, dtype=torch.float64)
+    G = torch.randn(2, 5, 3, dtype=torch.float64)
+    Rr = torch.randn(3, 3, dtype=torch.float64)
+    got = ops.precond_apply_two_sided(Lr.to(DEV), G.to(DEV), Rr.to(DEV))
+    assert torch.allclose(got.cpu(), Lr @ G @ Rr, atol=1e-12)
+
+
+# ------------------------------------------- the reference's own parity tests
+
+def test_reference_ns_parity(native_backend):
+    for shape in [(8, 5), (5, 8), (4, 6, 9)]:
+        G = torch.randn(*shape, device=DEV)
+        assert torch.allclose(ops.newton_schulz_orthogonalize(G), ops_ref.newton_schulz_orthogonalize(G), atol=1e-5)
+
+
+def test_reference_kron_parity(native_backend):
+    g = torch.Generator().manual_seed(12)
+    G1, G2 = (torch.randn(4, 7, generator=g).to(DEV) for _ in range(2))
+    for beta2 in (1.0, 0.9):
+        Ln, Rn = torch.zeros(4, 4, device=DEV), torch.zeros(7, 7, device=DEV)
+        Lr, Rr = torch.zeros(4, 4, device=DEV), torch.zeros(7, 7, device=DEV)
+        for G in (G1, G2):
+            ops.kron_factor_update_(Ln, Rn, G, beta2=beta2)
+            ops_ref.kron_factor_update_(Lr, Rr, G, beta2=beta2)
+        assert torch.allclose(Ln, Lr, atol=1e-6) and torch.allclose(Rn, Rr, atol=1e-6)
+
+
+def test_reference_apply_parity(native_backend):
+    Lr, G, Rr = torch.randn(4, 4, device=DEV), torch.randn(4, 7, device=DEV), torch.randn(7, 7, device=DEV)
+    assert torch.allclose(ops.precond_apply_two_sided(Lr, G, Rr), ops_ref.precond_apply_two_sided(Lr, G, Rr),
+                          atol=1e-6)
+
+
+def test_stream_ordering(native_backend):
+    """Kernels run on torch's current stream: a side stream's work is ordered
+    with the surrounding torch ops."""
+    s = torch.cuda.Stream()
+    G = torch.randn(256, 512, device=DEV)
+    with torch.cuda.stream(s):
+        H = G * 2.0
+        O = ops.newton_schulz_orthogonalize(H)
+        O2 = O * 1.0
+    s.synchronize()
+    want = oo.ns5((G * 2.0).cpu().numpy())
+    assert np.abs(O2.cpu().numpy() - want).max() < 1e-5

@@ -1,0 +1,205 @@
+"""Pins the numpy oracle against closed forms, the reference's own
+known-answer tests (tests/test_ops_reference.py of the reference) and brute
+force. Each check is chosen so a plausible slip (dropped term, wrong sign,
+transposed operand, wrong index) fails; several tests plant such a slip in
+the oracle and assert the check catches it."""
+
+import numpy as np
+import pytest
+
+from oracle import ops_oracle as oo
+
+A_, B_, C_ = oo.NS_COEFFS
+
+
+def _orth(n, rng):
+    q, r = np.linalg.qr(rng.standard_normal((n, n)))
+    return q * np.sign(np.diag(r))
+
+
+def _ns_closed_form(U, s, V, steps=5, coeffs=oo.NS_COEFFS, eps=1e-7):
+    """NS acts on each singular value independently: s/(‖s‖+eps) through
+    φ(x) = a x + b x³ + c x⁵, `steps` times."""
+    a, b, c = coeffs
+    x = s / (np.sqrt(np.sum(s * s)) + eps)
+    for _ in range(steps):
+        x = a * x + b * x ** 3 + c * x ** 5
+    return (U * x) @ V.T
+
+
+@pytest.mark.parametrize("shape", [(6, 10), (10, 6), (8, 8), (32, 48)])
+def test_ns5_closed_form(shape):
+    rng = np.random.default_rng(1)
+    m, n = shape
+    k = min(m, n)
+    U = _orth(m, rng)[:, :k]
+    V = _orth(n, rng)[:, :k]
+    s = np.exp(rng.uniform(-3, 0, size=k))
+    G = (U * s) @ V.T
+    want = _ns_closed_form(U, s, V)
+    got64 = oo.ns5(G.astype(np.float64))
+    assert np.abs(got64 - want).max() < 1e-10
+    got32 = oo.ns5(G.astype(np.float32))
+    assert np.abs(got32 - want).max() < 2e-5
+
+
+def test_ns5_closed_form_catches_planted_slips():
+    rng = np.random.default_rng(2)
+    U, V = _orth(8, rng), _orth(8, rng)
+    s = np.exp(rng.uniform(-2, 0, size=8))
+    G = (U * s) @ V.T
+    want = _ns_closed_form(U, s, V)
+    with np.errstate(over="ignore", invalid="ignore"):
+        for wrong in [(A_, -B_, C_), (A_, B_, 0.0), (A_, C_, B_)]:
+            assert not (np.abs(oo.ns5(G, coeffs=wrong) - want).max() < 1e-3)
+    # a transposed product (X·X instead of X·Xᵀ) on a non-symmetric input
+    X = G / np.linalg.norm(G)
+    bad = X
+    for _ in range(5):
+        A = bad @ bad
+        bad = A_ * bad + (B_ * A + C_ * A @ A) @ bad
+    assert np.abs(bad - want).max() > 1e-3
+
+
+def test_ns5_semi_orthogonal_gives_scalar_multiple():
+    # the reference's tests/test_ops_reference.py:72-80
+    rng = np.random.default_rng(3)
+    for shape in [(8, 8), (12, 6)]:
+        Q, _ = np.linalg.qr(rng.standard_normal(shape))
+        O = oo.ns5(Q.astype(np.float32), steps=10)
+        s = (O * Q).sum() / (Q * Q).sum()
+        assert 0.3 < s < 1.6
+        assert np.linalg.norm(O - s * Q) / np.linalg.norm(Q) < 1e-3
+
+
+def test_ns5_band_and_polar_distance():
+    # the reference's tests/test_ops_reference.py:62-69
+    rng = np.random.default_rng(4)
+    G = rng.standard_normal((16, 32)).astype(np.float32)
+    O = oo.ns5(G)
+    sv = np.linalg.svd(O.astype(np.float64), compute_uv=False)
+    assert sv.min() > 0.3 and sv.max() < 1.6
+    U, _, Vh = np.linalg.svd(G.astype(np.float64), full_matrices=False)
+    polar = U @ Vh
+    assert np.linalg.norm(O - polar) / np.linalg.norm(polar) < 0.35
+
+
+def test_ns5_batched_transpose_and_zero_steps():
+    rng = np.random.default_rng(5)
+    G = rng.standard_normal((4, 8, 12)).astype(np.float32)
+    O = oo.ns5(G)
+    for i in range(4):
+        np.testing.assert_allclose(O[i], oo.ns5(G[i]), atol=1e-6)
+    np.testing.assert_allclose(oo.ns5(G[0].T), O[0].T, atol=1e-6)
+    Z = oo.ns5(G[0], steps=0)
+    np.testing.assert_allclose(Z, G[0] / (np.linalg.norm(G[0]) + 1e-7), rtol=1e-6)
+    with pytest.raises(ValueError, match="ndim"):
+        oo.ns5(np.ones(3, dtype=np.float32))
+
+
+def test_ns5_flops():
+    # 5 iterations x (2·4096²·4097 + 2·4096³) = 1.3746e12
+    assert oo.ns5_flops(4096, 4096) == 10 * 4096 ** 2 * (4097 + 4096) == 1374557306880
+    assert oo.ns5_flops(4096, 11008) == oo.ns5_flops(11008, 4096)
+
+
+def test_kron_closed_forms():
+    # the reference's tests/test_ops_reference.py:92-108
+    rng = np.random.default_rng(6)
+    G1, G2 = rng.standard_normal((2, 4, 7))
+    L, R = np.zeros((4, 4)), np.zeros((7, 7))
+    L, R = oo.kron_factor_update(L, R, G1, 1.0)
+    L, R = oo.kron_factor_update(L, R, G2, 1.0)
+    outer_l = sum(np.outer(G[:, k], G[:, k]) for G in (G1, G2) for k in range(7))
+    outer_r = sum(np.outer(G[i, :], G[i, :]) for G in (G1, G2) for i in range(4))
+    np.testing.assert_allclose(L, outer_l, atol=1e-12)
+    np.testing.assert_allclose(R, outer_r, atol=1e-12)
+    b = 0.9
+    L, R = oo.kron_factor_update(np.zeros((4, 4)), np.zeros((7, 7)), G1, b)
+    L, R = oo.kron_factor_update(L, R, G2, b)
+    np.testing.assert_allclose(L, b * (1 - b) * G1 @ G1.T + (1 - b) * G2 @ G2.T, atol=1e-12)
+    np.testing.assert_allclose(R, b * (1 - b) * G1.T @ G1 + (1 - b) * G2.T @ G2, atol=1e-12)
+    with pytest.raises(ValueError, match="2D"):
+        oo.kron_factor_update(L, R, np.ones((2, 3, 4)))
+
+
+def _spd(n, seed, lo=0.5, hi=4.0):
+    rng = np.random.default_rng(seed)
+    Q = _orth(n, rng)
+    lam = np.linspace(lo, hi, n)
+    return (Q * lam) @ Q.T, Q, lam
+
+
+def test_inverse_root_closed_form():
+    # the reference's tests/test_ops_reference.py:16-21
+    A, Q, lam = _spd(6, 1)
+    for p in (1, 2, 4):
+        want = (Q * lam ** (-1.0 / p)) @ Q.T
+        got, _ = oo.inverse_root(A, p)
+        np.testing.assert_allclose(got, want, atol=1e-10)
+        got_n, iters = oo.inverse_root(A, p, method="newton")
+        np.testing.assert_allclose(got_n, want, atol=1e-9)
+        assert 1 <= iters < 100
+
+
+def test_newton_matches_eigh_and_damping():
+    # the reference's tests/test_ops_reference.py:24-38
+    A, _, _ = _spd(8, 3)
+    for p in (2, 3, 4, 5):
+        got_n, _ = oo.inverse_root(A, p, damping=1e-3, method="newton")
+        got_e, _ = oo.inverse_root(A, p, damping=1e-3, method="eigh")
+        np.testing.assert_allclose(got_n, got_e, atol=1e-7)
+    A5, _, _ = _spd(5, 4)
+    d = 0.37
+    np.testing.assert_allclose(oo.inverse_root(A5, 2, damping=d)[0], oo.inverse_root(A5 + d * np.eye(5), 2)[0],
+                               atol=1e-10)
+
+
+def test_newton_planted_slip_fails_residual():
+    A, _, _ = _spd(8, 7)
+    X, _ = oo.inverse_root(A, 4, method="newton")
+    assert oo.root_residual(X, A, 4) < 1e-9
+    assert oo.root_residual(X.T @ X, A, 4) > 1e-2  # a wrong power
+    assert oo.root_residual(X, A + 0.1 * np.eye(8), 4) > 1e-3  # missing damping term
+
+
+def test_batched_root_and_validation():
+    # the reference's tests/test_ops_reference.py:41-58
+    rng = np.random.default_rng(5)
+    B = rng.standard_normal((3, 5, 5))
+    A = (B @ np.swapaxes(B, -1, -2) + 0.1 * np.eye(5)).astype(np.float32)
+    got, _ = oo.inverse_root(A, 4)
+    assert got.dtype == np.float32 and got.shape == A.shape
+    for i in range(3):
+        np.testing.assert_allclose(got[i], oo.inverse_root(A[i].astype(np.float64), 4)[0], atol=1e-5)
+    with pytest.raises(ValueError, match="positive integer"):
+        oo.inverse_root(A, 0)
+    with pytest.raises(ValueError, match="method"):
+        oo.inverse_root(A, 2, method="qr")
+
+
+def test_matrix_power_order_matches_numpy():
+    rng = np.random.default_rng(8)
+    M = rng.standard_normal((6, 6))
+    for p in range(1, 9):
+        np.testing.assert_allclose(oo.matrix_power(M, p), np.linalg.matrix_power(M, p), rtol=1e-10, atol=1e-10)
+
+
+def test_gram_update_brute_force():
+    rng = np.random.default_rng(9)
+    X = rng.standard_normal((2, 5, 3)).astype(np.float64)  # rows flattened over leading dims
+    rows = X.reshape(-1, 3)
+    aug = np.concatenate([rows, np.ones((10, 1))], axis=1)
+    want = sum(np.outer(r, r) for r in aug) / 10
+    got = oo.gram_update(None, X, beta=0.0, alpha=0.1, append_ones=True, dtype=np.float64)
+    np.testing.assert_allclose(got, want, atol=1e-12)
+    F0 = rng.standard_normal((4, 4))
+    got = oo.gram_update(F0, X, beta=0.95, alpha=0.05 / 10, append_ones=True, dtype=np.float64)
+    np.testing.assert_allclose(got, 0.95 * F0 + 0.05 * want, atol=1e-12)
+
+
+def test_precond_apply_brute_force():
+    rng = np.random.default_rng(10)
+    L, G, R = rng.standard_normal((4, 4)), rng.standard_normal((4, 7)), rng.standard_normal((7, 7))
+    want = np.einsum("ij,jk,kl->il", L, G, R)
+    np.testing.assert_allclose(oo.precond_apply(L, G, R), want, atol=1e-12)
