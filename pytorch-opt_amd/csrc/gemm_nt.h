@@ -16,9 +16,8 @@
 // for (i, j), i <= j, is stored at (i, j) and at (j, i), so the result is an
 // exactly symmetric matrix at half the MFMA work.
 //
-// Pipeline: two LDS stages; the global loads of tile k+1 are issued into
-// registers before the MFMAs of tile k and written to the other LDS stage
-// afterwards, so one barrier per K tile suffices.
+// Pipeline: a ring of four LDS stages filled by direct global-to-LDS loads,
+// three K tiles ahead of the MFMAs; one barrier per K tile (details below).
 #pragma once
 
 #include "pto_common.h"
@@ -80,7 +79,7 @@ struct Mfma<double> {  // v_mfma_f64_16x16x4_f64
   __device__ static __forceinline__ int col(int lane, int) { return lane & 15; }
 };
 
-// Tile configuration: BM x BN output tile, BK deep, WM x WN waves.
+// Tile configuration: BM x BN output tile, BK deep (64 bytes), WM x WN waves.
 template <int BM_, int BN_, int BK_, int WM_, int WN_>
 struct Tile {
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
@@ -96,6 +95,17 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   const int* guard;  // if non-null and *guard != 0 the launch does nothing
 };
+
+// Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each
+// XCD has its own L2. Renumber so that XCD x runs one contiguous range of
+// logical tiles: the ~32 tiles co-resident on an XCD are then neighbours in
+// the (batch, tile) order and share operand panels in that XCD's L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_remap(int w, int total) {
+  const int q = total / kXcds, r = total % kXcds;
+  const int xcd = w % kXcds, slot = w / kXcds;
+  return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}
 
 // Map the linear tile id to (tile_row, tile_col).
 template <bool UPPER>
@@ -121,77 +131,128 @@ __device__ __forceinline__ void decode_tile(int t, int tiles_m, int tiles_n, int
   }
 }
 
+// ------------------------------------------------------------- main loop
+// K tiles are 64 bytes deep (bf16 BK=32, fp32 16, fp64 8). Operand tiles
+// go from global memory straight into LDS (global_load_lds_dwordx4: each
+// wave instruction fills 1 KiB = 16 rows of 64 bytes) through a ring of
+// four stages, so three tiles are in flight while one is consumed, with no
+// staging registers and no ds_write instructions. The stages are separate
+// __shared__ arrays and the loop is unrolled by four, so every LDS access
+// names its stage statically and the compiler's wait insertion can tell the
+// in-flight stages apart; prefetches are unconditional (past the end they
+// re-read the last tile into a stage that is never consumed) so the
+// outstanding-load count is the same on every path.
+//
+// LDS rows are unpadded; 16-byte chunk c of row r lives at physical chunk
+// c ^ f(r), f(r) = ((r >> 2) & 3) ^ (r & 2), which makes the fragment
+// reads (16 consecutive rows, one chunk) conflict-free in both 8- and
+// 16-lane windows. The DMA side needs no care: it writes 1 KiB runs.
+constexpr int kStages = 4;
+constexpr int kRowBytes = 64;
+
+__device__ __forceinline__ int swz(int r) { return ((r >> 2) & 3) ^ (r & 2); }
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 layout:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+#define PTO_VMCNT(n) ((((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8)))
+// ... and with only lgkmcnt(0) required.
+#define PTO_LGKM0 ((0xF) | (3 << 14) | (0x7 << 4))
+
+// All waves' earlier LDS reads are done and their waited-for DMA writes
+// visible. A bare s_barrier (no release fence, which would force every
+// in-flight load to complete) bracketed by compiler-only fences.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void gbl_void_t;
+
+// LDS plan: four stages of (BM + BN) rows x 64 bytes; after the loop each
+// stage array also hosts the epilogue staging of WPA waves (RPP rows x
+// (WTN + 1) accumulator-type values per wave, odd pitch).
+template <typename T, class Cfg, typename S>
+struct LdsPlan {
+  static constexpr int NW = Cfg::WM * Cfg::WN;
+  static constexpr int WTM = Cfg::BM / Cfg::WM, WTN = Cfg::BN / Cfg::WN;
+  static constexpr int STAGE = (Cfg::BM + Cfg::BN) * kRowBytes;
+  static constexpr int WPA = (NW + kStages - 1) / kStages;  // waves per array in the epilogue
+  static constexpr int RPP = WTM < 64 ? WTM : 64;            // rows per epilogue pass
+  static constexpr int SP = WTN + 1;
+  static constexpr int EPI = WPA * RPP * SP * (int)sizeof(S);
+  static constexpr int ARR = ((STAGE > EPI ? STAGE : EPI) + 15) / 16 * 16;
+};
+
 template <typename T, class Cfg, bool UPPER, class Epi>
 __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   typedef Mfma<T> MF;
   typedef typename MF::cvec_t cvec_t;
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, BK = Cfg::BK, NT = Cfg::NT;
-  constexpr int VEC = 16 / sizeof(T);       // elements per 16-byte chunk
-  constexpr int CPR = BK / VEC;             // chunks per tile row
-  constexpr int PITCH = BK + VEC;           // LDS row pitch (16-byte pad)
-  constexpr int WTM = BM / Cfg::WM, WTN = BN / Cfg::WN;
+  typedef typename Epi::S S;
+  typedef LdsPlan<T, Cfg, S> Plan;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT, NW = Plan::NW;
+  constexpr int BK = kRowBytes / (int)sizeof(T);   // elements per K tile
+  constexpr int VEC = 16 / (int)sizeof(T);         // elements per 16-byte chunk
+  constexpr int WTM = Plan::WTM, WTN = Plan::WTN;
   constexpr int FM = WTM / MF::MN, FN = WTN / MF::MN;
-  constexpr int LP = BM * CPR / NT, LQ = BN * CPR / NT;
-  constexpr int KSPAN = BK / MF::G;         // k values per lane group per tile
-  constexpr int NRG = KSPAN / VEC;          // 16-byte reads per fragment per tile
-  constexpr int IPR = VEC / MF::KPL;        // instructions per 16-byte read
-  static_assert(BK * sizeof(T) == 128, "tiles are 128 bytes deep");
-  static_assert(BM * CPR % NT == 0 && BN * CPR % NT == 0, "load split");
-  static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0, "wave tile");
-  static_assert(KSPAN % VEC == 0, "fragment runs");
+  constexpr int KSPAN = BK / MF::G;                // k values per lane group per tile
+  constexpr int NRG = KSPAN / VEC;                 // 16-byte fragment reads per tile
+  constexpr int IPR = VEC / MF::KPL;               // MFMAs per 16-byte read
+  constexpr int IPW = (BM + BN) / 16 / NW;         // DMA instructions per wave per tile
+  static_assert((BM + BN) % (16 * NW) == 0 && IPW >= 1, "DMA split");
+  static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0 && WTM % 16 == 0, "wave tile");
+  static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
+  static_assert(3 * IPW <= 63, "vmcnt range");
 
   if (g.guard != nullptr && *g.guard != 0) return;
 
-  __shared__ __attribute__((aligned(16))) T lds[2][(BM + BN) * PITCH];
+  __shared__ __attribute__((aligned(16))) char st0[Plan::ARR];
+  __shared__ __attribute__((aligned(16))) char st1[Plan::ARR];
+  __shared__ __attribute__((aligned(16))) char st2[Plan::ARR];
+  __shared__ __attribute__((aligned(16))) char st3[Plan::ARR];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
-  const int b = blockIdx.y;
+  const int ntile = gridDim.x;  // tiles per matrix
+  const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y);
+  const int b = logical / ntile;
   int ti, tj;
-  decode_tile<UPPER>(blockIdx.x, g.tiles_m, g.tiles_n, ti, tj);
+  decode_tile<UPPER>(logical - b * ntile, g.tiles_m, g.tiles_n, ti, tj);
   const int row0 = ti * BM, col0 = tj * BN;
 
-  const T* __restrict__ P = static_cast<const T*>(g.P) + (int64_t)b * g.sP;
-  const T* __restrict__ Q = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ;
-
-  // Per-thread global source pointers (nullptr = masked row).
-  const T* src_p[LP];
-  const T* src_q[LQ];
+  // Per-thread DMA sources: instruction q of this wave fills stage rows
+  // R0 = 16*(wave*IPW + q) .. +15 (P rows first, then Q rows); this lane
+  // supplies row R0 + lane/4, physical chunk lane%4, i.e. logical chunk
+  // (lane%4) ^ swz(row). Rows past M (N) re-read the last valid row.
+  const T* src[IPW];
+  int dst_off[IPW];
 #pragma unroll
-  for (int q = 0; q < LP; ++q) {
-    int c = tid + q * NT, r = c / CPR, kc = c % CPR;
-    int gr = row0 + r;
-    src_p[q] = gr < g.M ? P + (int64_t)gr * g.ldp + kc * VEC : nullptr;
-  }
-#pragma unroll
-  for (int q = 0; q < LQ; ++q) {
-    int c = tid + q * NT, r = c / CPR, kc = c % CPR;
-    int gr = col0 + r;
-    src_q[q] = gr < g.N ? Q + (int64_t)gr * g.ldq + kc * VEC : nullptr;
-  }
-
-  uint4 rp[LP], rq[LQ];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int q = 0; q < LP; ++q)
-      rp[q] = src_p[q] ? *reinterpret_cast<const uint4*>(src_p[q] + k0) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int q = 0; q < LQ; ++q)
-      rq[q] = src_q[q] ? *reinterpret_cast<const uint4*>(src_q[q] + k0) : make_uint4(0, 0, 0, 0);
-  };
-  auto lstore = [&](int s) {
-    T* L = lds[s];
-#pragma unroll
-    for (int q = 0; q < LP; ++q) {
-      int c = tid + q * NT, r = c / CPR, kc = c % CPR;
-      *reinterpret_cast<uint4*>(L + r * PITCH + kc * VEC) = rp[q];
+  for (int q = 0; q < IPW; ++q) {
+    const int R0 = 16 * (wave * IPW + q), r = R0 + (lane >> 2);
+    const int chunk = (lane & 3) ^ swz(r);
+    const T* base;
+    int64_t ld;
+    int gr;
+    if (R0 < BM) {
+      base = static_cast<const T*>(g.P) + (int64_t)b * g.sP;
+      ld = g.ldp;
+      gr = min(row0 + r, max(g.M - 1, 0));
+    } else {
+      base = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ;
+      ld = g.ldq;
+      gr = min(col0 + (r - BM), max(g.N - 1, 0));
     }
+    src[q] = base + (int64_t)gr * ld + chunk * VEC;
+    dst_off[q] = R0 * kRowBytes;
+  }
+  auto issue = [&](int kt, char* stage) {
 #pragma unroll
-    for (int q = 0; q < LQ; ++q) {
-      int c = tid + q * NT, r = c / CPR, kc = c % CPR;
-      *reinterpret_cast<uint4*>(L + (BM + r) * PITCH + kc * VEC) = rq[q];
-    }
+    for (int q = 0; q < IPW; ++q)
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(src[q] + (int64_t)kt * BK), (lds_void_t*)(stage + dst_off[q]),
+                                       16, 0, 0);
   };
 
   cvec_t acc[FM][FN];
@@ -203,19 +264,20 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       for (int r = 0; r < MF::NACC; ++r) acc[fm][fn][r] = 0;
 
   const int lr = lane % MF::MN, lg = lane / MF::MN;
-  auto compute = [&](int s) {
-    const T* L = lds[s];
-    const T* Pw = L + (wm * WTM + lr) * PITCH + lg * KSPAN;
-    const T* Qw = L + (BM + wn * WTN + lr) * PITCH + lg * KSPAN;
+  const int sw = swz(lr);  // rows of every fragment are lr mod 16
+  auto compute = [&](const char* stage) {
+    const char* Pw = stage + (wm * WTM + lr) * kRowBytes;
+    const char* Qw = stage + (BM + wn * WTN + lr) * kRowBytes;
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
+      const int off = ((lg * NRG + rg) ^ sw) * 16;
       uint4 a[FM], bq[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
-        a[fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * PITCH + rg * VEC);
+        a[fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
-        bq[fn] = *reinterpret_cast<const uint4*>(Qw + fn * MF::MN * PITCH + rg * VEC);
+        bq[fn] = *reinterpret_cast<const uint4*>(Qw + fn * MF::MN * kRowBytes + off);
 #pragma unroll
       for (int ii = 0; ii < IPR; ++ii)
 #pragma unroll
@@ -227,126 +289,140 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 
   const int KT = g.K / BK;
   if (KT > 0) {
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < KT; ++kt) {
-      const int cur = kt & 1;
-      if (kt + 1 < KT) gload((kt + 1) * BK);
-      compute(cur);
-      if (kt + 1 < KT) lstore(cur ^ 1);
-      __syncthreads();
+    issue(0, st0);
+    issue(min(1, KT - 1), st1);
+    issue(min(2, KT - 1), st2);
+    for (int kt = 0; kt < KT; kt += kStages) {
+#define PTO_STEP(J, CUR, NXT)                                 \
+  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));             \
+  stage_barrier();                                            \
+  issue(min(kt + (J) + 3, KT - 1), NXT);                      \
+  if (kt + (J) < KT) compute(CUR);
+      PTO_STEP(0, st0, st3)
+      PTO_STEP(1, st1, st0)
+      PTO_STEP(2, st2, st1)
+      PTO_STEP(3, st3, st2)
+#undef PTO_STEP
     }
+    __builtin_amdgcn_s_waitcnt(PTO_VMCNT(0));  // stray prefetches land before reuse
+    stage_barrier();
   }
 
-  // Epilogue, staged through LDS (free after the last barrier above) in
-  // chunks of CH tile rows, so every global access of the functor is a run
-  // of up to 8 consecutive elements of one output row:
-  //   1. waves owning the chunk's rows write raw accumulators to LDS;
+  // Epilogue, per wave and staged through LDS so every global access of the
+  // functor is a run of up to 8 consecutive elements of one output row.
+  // Each wave owns a private slice (RPP rows of its WTM x WTN sub-tile at a
+  // time), so no cross-wave synchronisation is needed:
+  //   1. the wave writes RPP rows of raw accumulators to its slice;
   //   2. direct pass: runs along output rows (i, j..j+7) -> epi.put, which
   //      hands back the value the transposed pass should see;
   //   3. transposed pass (mirror of a symmetric tile, or the functor's
   //      transposed copy): runs along (j, i..i+7) -> epi.put_t.
-  // In symmetric (UPPER) products only i <= j is taken from the MFMA result;
-  // on diagonal tiles the direct pass stores i <= j and the transposed pass
-  // i > j, so the stored matrix is exactly symmetric.
-  typedef typename Epi::S S;
-  constexpr int SP = BN + 1;  // staging pitch (≡ 1 mod 64 banks for BN >= 64)
-  constexpr int LDS_BYTES = 2 * (BM + BN) * PITCH * (int)sizeof(T);
-  constexpr int CH_FIT = LDS_BYTES / (SP * (int)sizeof(S));
-  constexpr int CH = CH_FIT >= BM ? BM : (CH_FIT / WTM) * WTM;
-  static_assert(CH >= WTM && BM % CH == 0, "epilogue chunk");
-  constexpr int CPRW = BN / 8;                 // 8-element runs per tile row
-  constexpr int LGD = CPRW < 8 ? CPRW : 8;     // lanes sharing a row in a 64-item block
-  constexpr int RPB = 64 / LGD;                // rows per 64-item block
-  constexpr int CBLK = CPRW / LGD;             // 64-item blocks across a row
-  S* stg = reinterpret_cast<S*>(&lds[0][0]);
+  // In symmetric (UPPER) products the value for (i, j), i <= j, is stored
+  // at (i, j) by its own direct pass and at (j, i) by its transposed pass;
+  // on diagonal tiles positions below the diagonal are skipped by the
+  // direct pass, so the stored matrix is exactly symmetric.
+  constexpr int RPP = Plan::RPP, SP = Plan::SP;
+  char* arr = (wave / Plan::WPA) == 0 ? st0 : (wave / Plan::WPA) == 1 ? st1 : (wave / Plan::WPA) == 2 ? st2 : st3;
+  S* stg = reinterpret_cast<S*>(arr) + (wave % Plan::WPA) * RPP * SP;
   const bool diag = UPPER && ti == tj;
   const bool need_t = UPPER || epi.has_t();
-  const int mrem = g.M - row0, nrem = g.N - col0;  // valid extent of this tile
-
-  for (int c0 = 0; c0 < BM; c0 += CH) {
-    if (c0 >= mrem) break;
-    const int wr0 = wm * WTM;
-    if (wr0 >= c0 && wr0 < c0 + CH) {
+  const int wr0 = row0 + wm * WTM, wc0 = col0 + wn * WTN;  // sub-tile origin
+  const int nrem = g.N - wc0;
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+  for (int hp = 0; hp < WTM / RPP; ++hp) {
+    const int pr0 = wr0 + hp * RPP;  // first output row of this pass
+    if (pr0 >= g.M || nrem <= 0) break;
+    const int rows = min(RPP, g.M - pr0);
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
+    for (int fm = hp * (RPP / MF::MN); fm < (hp + 1) * (RPP / MF::MN); ++fm)
 #pragma unroll
-          for (int r = 0; r < MF::NACC; ++r) {
-            const int li = wr0 - c0 + fm * MF::MN + MF::row(lane, r);
-            const int lj = wn * WTN + fn * MF::MN + MF::col(lane, r);
-            stg[li * SP + lj] = static_cast<S>(acc[fm][fn][r]);
-          }
-    }
-    __syncthreads();
-    const int rows = min(CH, mrem - c0);
-    // direct pass: item -> (row lr, run lc); 8 lanes cover 64 consecutive
-    // columns of one row, and the odd pitch keeps the LDS reads conflict-free
-    const int dblocks = ((rows + RPB - 1) / RPB) * CBLK;
-    for (int t = tid; t < dblocks * 64; t += NT) {
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < MF::NACC; ++r) {
+          const int li = fm * MF::MN - hp * RPP + MF::row(lane, r);
+          const int lj = fn * MF::MN + MF::col(lane, r);
+          stg[li * SP + lj] = static_cast<S>(acc[fm][fn][r]);
+        }
+    __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+    __builtin_amdgcn_wave_barrier();
+    // direct pass: 8 lanes cover 64 consecutive columns of one row
+    constexpr int RUNS = WTN / 8;                  // 8-element runs per row
+    constexpr int LGD = RUNS < 8 ? RUNS : 8;
+    constexpr int RPB = 64 / LGD;
+    constexpr int CBLK = RUNS / LGD;
+    for (int t = lane; t < ((RPP + RPB - 1) / RPB) * CBLK * 64; t += 64) {
       const int blk = t >> 6, w = t & 63;
-      const int lr = (blk / CBLK) * RPB + w / LGD;
-      const int lc = ((blk % CBLK) * LGD + w % LGD) * 8;
-      if (lr >= rows || lc >= nrem) continue;
-      const int n = min(8, nrem - lc);
-      const int kbeg = diag ? max(0, c0 + lr - lc) : 0;  // skip i > j on diagonal tiles
+      const int r = (blk / CBLK) * RPB + w / LGD;
+      const int c = ((blk % CBLK) * LGD + w % LGD) * 8;
+      if (r >= rows || c >= nrem) continue;
+      const int i = pr0 + r, j0 = wc0 + c;
+      const int n = min(8, nrem - c);
+      const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
       if (kbeg >= n) continue;
       S v[8], vo[8];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = stg[lr * SP + lc + k];
-      epi.put(b, row0 + c0 + lr, col0 + lc, v, kbeg, n, vo);
+      for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
+      epi.put(b, i, j0, v, kbeg, n, vo);
       if (need_t) {
 #pragma unroll
-        for (int k = 0; k < 8; ++k) stg[lr * SP + lc + k] = vo[k];
+        for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];
       }
     }
     if (need_t) {
-      __syncthreads();
-      // transposed pass: output row j = col0 + lc, columns i = row0+c0+lr..+7;
-      // 8 lanes share lc and cover 64 consecutive i
+      __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+      __builtin_amdgcn_wave_barrier();
+      // transposed pass: output row j = wc0 + c, columns i = pr0 + r..r+7;
+      // 8 lanes share c and cover 64 consecutive i
       const int rgroups = (rows + 7) / 8;
-      const int tblocks = ((rgroups + 7) / 8) * CPRW;
-      for (int t = tid; t < tblocks * 64; t += NT) {
+      for (int t = lane; t < ((rgroups + 7) / 8) * WTN * 8; t += 64) {
         const int blk = t >> 6, w = t & 63;
-        const int lc = (blk % CPRW) * 8 + w / 8;
-        const int lr = ((blk / CPRW) * 8 + w % 8) * 8;
-        if (lc >= nrem || lr >= rows) continue;
-        int n = min(8, rows - lr);
-        if (diag) n = min(n, lc - (c0 + lr));  // strictly below the diagonal
+        const int c = (blk % (WTN / 8)) * 8 + w / 8;
+        const int r = ((blk / (WTN / 8)) * 8 + w % 8) * 8;
+        if (c >= nrem || r >= rows) continue;
+        const int j = wc0 + c, i0 = pr0 + r;
+        int n = min(8, rows - r);
+        if (diag) n = min(n, j - i0);  // strictly below the diagonal
         if (n <= 0) continue;
         S v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(lr + k) * SP + lc] : S(0);
-        epi.put_t(b, col0 + lc, row0 + c0 + lr, v, n);
+        for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(r + k) * SP + c] : S(0);
+        epi.put_t(b, j, i0, v, n);
       }
     }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+    __builtin_amdgcn_wave_barrier();
   }
   epi.finish(b);
 }
 
 // ------------------------------------------------------------- host launch
 
-// Tile choices per element type. "big" for large problems, "small" when
-// the big tiles would leave most of the 256 CUs idle.
+// Tile choices per element type: full products and symmetric (upper-tile)
+// products, each with a "big" tile for large problems and a "small" one
+// when the big tiles would leave most of the 256 CUs idle. Symmetric
+// products need square tiles.
 template <typename T>
 struct TileSet;
 template <>
 struct TileSet<bf16> {
-  typedef Tile<256, 256, 64, 2, 4> big;
-  typedef Tile<128, 128, 64, 2, 2> small;
+  typedef Tile<256, 256, 32, 2, 4> big;
+  typedef Tile<128, 128, 32, 2, 2> small;
+  typedef Tile<256, 256, 32, 2, 4> sym_big;
+  typedef Tile<128, 128, 32, 2, 2> sym_small;
 };
 template <>
 struct TileSet<float> {
-  typedef Tile<128, 128, 32, 2, 2> big;
-  typedef Tile<64, 64, 32, 2, 2> small;
+  typedef Tile<128, 128, 16, 2, 2> big;
+  typedef Tile<64, 64, 16, 2, 2> small;
+  typedef big sym_big;
+  typedef small sym_small;
 };
 template <>
 struct TileSet<double> {
-  typedef Tile<64, 64, 16, 2, 2> big;
-  typedef Tile<32, 32, 16, 2, 2> small;
+  typedef Tile<64, 64, 8, 2, 2> big;
+  typedef Tile<32, 32, 8, 2, 2> small;
+  typedef big sym_big;
+  typedef small sym_small;
 };
 
 template <typename T, class Cfg, bool UPPER, class Epi>
@@ -363,11 +439,23 @@ int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, c
   return 0;
 }
 
+template <typename T, bool UPPER>
+struct PickTiles {
+  typedef typename TileSet<T>::big Big;
+  typedef typename TileSet<T>::small Small;
+};
+template <typename T>
+struct PickTiles<T, true> {
+  typedef typename TileSet<T>::sym_big Big;
+  typedef typename TileSet<T>::sym_small Small;
+};
+
 // Validate the operand contract and pick a tile size.
 template <typename T, bool UPPER, class Epi>
 int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
-  typedef typename TileSet<T>::big Big;
-  typedef typename TileSet<T>::small Small;
+  typedef typename PickTiles<T, UPPER>::Big Big;
+  typedef typename PickTiles<T, UPPER>::Small Small;
+  static_assert(!UPPER || (Big::BM == Big::BN && Small::BM == Small::BN), "symmetric products need square tiles");
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
   PTO_REQUIRE(!UPPER || g.M == g.N, std::string(name) + ": symmetric product needs M == N");
   PTO_REQUIRE(g.K % Small::BK == 0 && g.K % Big::BK == 0, std::string(name) + ": K not padded");
