@@ -1,15 +1,23 @@
-"""Benchmark: batched bf16 Newton–Schulz (NS5) on one MI355X.
+"""Benchmark of the pytorch_opt.ops hot path on one MI355X.
 
-Workload (one "step"): NS5, 5 quintic iterations, on 32 bf16 matrices
-4096x4096 plus 32 bf16 matrices 4096x11008 (Llama-7B-like projection
-shapes), inputs = Nesterov momentum (β=0.95) of three seeded N(0, 1e-3)
-gradients, resident in HBM before timing. Two batched calls of
-pytorch_opt.ops.newton_schulz_orthogonalize through the HIP library.
+Headline workload (one "step"): NS5, 5 quintic iterations, on 32 bf16
+matrices 4096x4096 plus 32 bf16 matrices 4096x11008 (Llama-7B-like
+projection shapes); inputs are the Nesterov momentum (β=0.95) of three
+seeded N(0, 1e-3) gradients, resident in HBM before timing. Two batched calls
+of pytorch_opt.ops.newton_schulz_orthogonalize through the HIP library.
 
-Prints one JSON line: the metric (algorithmic TFLOP/s, LAWN-41 counting),
-the roofline of the dominant kernel (timed live with HIP events on its own
-stream), the CPU oracle's rate on a bounded sample of the same workload,
-and the single-matrix 4096² figure.
+The JSON line carries the headline (algorithmic TFLOP/s, LAWN-41 counting),
+the roofline of the dominant kernel (HIP events recorded on its launch
+stream inside the library), the numpy CPU oracle on a bounded sample of the
+same workload, and secondary figures:
+  single_4096   one 4096x4096 NS5;
+  factors       Kronecker EMA update of fp32 G 4096² and the K-FAC Gram
+                AᵀA/n of bf16 A 16384x4096 into fp32;
+  roots         inverse 4th roots (coupled Newton, fp32) of SPD n = 1024 /
+                2048 / 4096 with λ log-uniform in [1e-6, 1], ε = 1e-6;
+  optimizer     Muon + Shampoo steps on the synthetic 12-layer d=2048
+                parameter set (40 steps each), with the CPU oracle's
+                per-step estimate from a bounded sample.
 """
 
 from __future__ import annotations
@@ -26,7 +34,7 @@ for _p in (ROOT, os.path.join(ROOT, "pytorch-opt_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 flop/clk)
+PEAK = {"bf16": 2516.6, "fp32": 157.3, "fp64": 78.6}  # MI355X dense MFMA TFLOP/s
 SHAPES = [(32, 4096, 4096, 1000), (32, 4096, 11008, 2000)]  # (batch, rows, cols, seed base)
 
 
@@ -35,13 +43,37 @@ def ns5_flops(m, n, steps=5):
     return steps * (m * (m + 1) * n + m * m * (m + 1) + 2 * m * m * n)
 
 
-def kernel_flops(kind, m, n):
+def ns5_kernel_flops(kind, m, n):
     """Algorithmic flops of one NS5 iteration's launch of `kind`, per matrix."""
     m, n = min(m, n), max(m, n)
     return {"ns5_gram": m * (m + 1) * n, "ns5_square": m * m * (m + 1), "ns5_update": 2 * m * m * n}[kind]
 
 
-def make_inputs(torch, batch, rows, cols, seed0, dev):
+def blas_threads():
+    from threadpoolctl import threadpool_info
+
+    return int(max([d.get("num_threads", 1) for d in threadpool_info() if d.get("user_api") == "blas"] or [1]))
+
+
+def cpu_model():
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True).stdout
+        return next((l.split(":", 1)[1].strip() for l in out.splitlines() if l.startswith("Model name")), "")
+    except Exception:
+        return ""
+
+
+def timed(fn, reps=1):
+    fn()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    return (time.perf_counter() - t0) / reps
+
+
+# ------------------------------------------------------------ headline (config 2)
+
+def make_ns5_inputs(torch, batch, rows, cols, seed0, dev):
     out = torch.empty(batch, rows, cols, dtype=torch.bfloat16, device=dev)
     for i in range(batch):
         g = torch.Generator(device=dev).manual_seed(seed0 + i)
@@ -54,33 +86,228 @@ def make_inputs(torch, batch, rows, cols, seed0, dev):
     return out
 
 
-def cpu_baseline(inputs):
-    """The numpy oracle (fp32, OpenBLAS) on one matrix of each shape, scaled
-    linearly to the 32 + 32 batch."""
-    import numpy as np
-    from threadpoolctl import threadpool_info
-
+def cpu_baseline_ns5(inputs):
+    """Numpy oracle (fp32, OpenBLAS) on one matrix of each shape, scaled x32."""
     from oracle import ops_oracle as oo
 
-    threads = max([d.get("num_threads", 1) for d in threadpool_info() if d.get("user_api") == "blas"] or [1])
     total_s = 0.0
-    for (batch, rows, cols, _), G in zip(SHAPES, inputs):
+    for (batch, _, _, _), G in zip(SHAPES, inputs):
         x = G[0].float().cpu().numpy()
-        oo.ns5(x[:256, :512])  # warm the BLAS threads
-        t0 = time.perf_counter()
-        oo.ns5(x)
-        total_s += (time.perf_counter() - t0) * batch
+        total_s += timed(lambda: oo.ns5(x)) * batch
     flops = sum(b * ns5_flops(r, c) for b, r, c, _ in SHAPES)
-    try:
-        model = subprocess.run(["bash", "-c", "lscpu | grep 'Model name' | head -1"], capture_output=True,
-                               text=True).stdout.split(":", 1)[-1].strip()
-    except Exception:
-        model = ""
-    return {"value": flops / total_s / 1e12, "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
-            "sample": "oracle NS5 (numpy fp32) on 1 matrix 4096x4096 + 1 matrix 4096x11008 of the same inputs, "
-                      f"time scaled x32 each; est. full workload {total_s:.1f} s; host {model}, nproc "
-                      f"{os.cpu_count()}"}
+    return {"value": round(flops / total_s / 1e12, 4), "unit": "TFLOP/s", "cores": blas_threads(), "kind": "port",
+            "sample": "oracle NS5 (numpy fp32, OpenBLAS) on 1 matrix 4096x4096 + 1 matrix 4096x11008 of the same "
+                      f"inputs, time x32 each: est. {total_s:.1f} s for the full workload; host {cpu_model()}, "
+                      f"nproc {os.cpu_count()}"}
 
+
+# ------------------------------------------------------------ config 3 / 4
+
+def bench_factors(torch, ops, hip, dev, cpu):
+    """Kronecker EMA update (fp32 G 4096², β 0.95) and K-FAC Gram (bf16 A 16384x4096)."""
+    import numpy as np
+
+    g = torch.Generator(device=dev).manual_seed(2)
+    G0 = 1e-2 * torch.randn(4096, 4096, generator=g, device=dev)
+    G = 1e-2 * torch.randn(4096, 4096, generator=g, device=dev)
+    L, R = G0 @ G0.T, G0.T @ G0
+    g3 = torch.Generator(device=dev).manual_seed(3)
+    A = torch.randn(16384, 4096, generator=g3, device=dev).bfloat16()
+    F = torch.zeros(4096, 4096, device=dev)
+    res = {}
+    for name, fn, flops, peak, kinds in [
+        ("kron_update_fp32_4096", lambda: ops.kron_factor_update_(L, R, G, beta2=0.95), 2 * 4096 * 4097 * 4096,
+         "fp32", ("kron_left", "kron_right")),
+        ("kfac_gram_bf16_16384x4096", lambda: ops.gram_update_(F, A, beta=0.95, alpha=0.05 / 16384),
+         4096 * 4097 * 16384, "bf16", ("gram_update",))]:
+        fn()
+        torch.cuda.synchronize()
+        hip.prof_reset()
+        hip.prof_enable(True)
+        reps = 10
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / reps
+        hip.prof_enable(False)
+        kms = sum(hip.prof_query(k)[0] for k in kinds) / reps
+        res[name] = {"ms": round(wall * 1e3, 3), "kernel_ms": round(kms, 3),
+                     "tflops": round(flops / wall / 1e12, 2),
+                     "pct_peak": round(100 * flops / wall / 1e12 / PEAK[peak], 2), "peak_dtype": peak}
+    if cpu:
+        from oracle import ops_oracle as oo
+
+        Gc, Lc, Rc = G.cpu().numpy(), L.cpu().numpy(), R.cpu().numpy()
+        t = timed(lambda: oo.kron_factor_update(Lc, Rc, Gc, 0.95))
+        res["kron_update_fp32_4096"]["cpu_ms"] = round(t * 1e3, 1)
+        Ac = A[:4096].float().cpu().numpy()  # a quarter of the tokens, scaled x4
+        t = timed(lambda: oo.gram_update(None, Ac, 0.0, 1.0)) * 4
+        res["kfac_gram_bf16_16384x4096"]["cpu_ms"] = round(t * 1e3, 1)
+        res["cpu_note"] = "numpy oracle fp32; the Gram times 4096 of the 16384 rows and scales x4"
+    return res
+
+
+def bench_roots(torch, hip, dev, cpu):
+    """Coupled-Newton inverse 4th roots, fp32, n = 1024 / 2048 / 4096."""
+    res = {}
+    for n in (1024, 2048, 4096):
+        g = torch.Generator().manual_seed(4)
+        Q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+        g5 = torch.Generator().manual_seed(5)
+        lam = 10 ** (-6 * torch.rand(n, generator=g5, dtype=torch.float64))
+        A = ((Q * lam) @ Q.T).float().to(dev)
+        hip.inverse_matrix_root_iters(A, 4, 1e-6, "newton", False, 100, 1e-10)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        X, iters = hip.inverse_matrix_root_iters(A, 4, 1e-6, "newton", False, 100, 1e-10)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        Xd = X.double()
+        X2 = Xd @ Xd
+        M = A.double() + 1e-6 * torch.eye(n, dtype=torch.float64, device=dev)
+        resid = float(((X2 @ X2) @ M - torch.eye(n, dtype=torch.float64, device=dev)).norm() / n ** 0.5)
+        it_flops = 2 * n ** 3 + 3 * n * n * (n + 1)  # X·Mi full; Mi², Mi⁴, Mi⁴·Mk symmetric
+        entry = {"ms": round(wall * 1e3, 2), "iterations": iters, "ms_per_iter": round(wall * 1e3 / max(iters, 1), 3),
+                 "residual": float(f"{resid:.4e}"),
+                 "tflops": round(iters * it_flops / wall / 1e12, 2)}
+        if cpu and n == 1024:
+            from oracle import ops_oracle as oo
+
+            Ac = A.cpu().numpy()
+            t0 = time.perf_counter()
+            Xo, it_o = oo.inverse_root(Ac, 4, damping=1e-6, method="newton", root_dtype=__import__("numpy").float32)
+            t = time.perf_counter() - t0
+            entry["cpu_ms"] = round(t * 1e3, 1)
+            entry["cpu_iterations"] = it_o
+            entry["cpu_residual"] = float(f"{float(oo.root_residual(Xo, Ac, 4, 1e-6)):.4e}")
+        res[f"n{n}"] = entry
+    return res
+
+
+# ------------------------------------------------------------ config 5
+
+def config5_shapes():
+    mats, vecs = [], []
+    for l in range(12):
+        for nm in ("q", "k", "v", "o"):
+            mats.append((f"l{l}.{nm}", (2048, 2048), "attn"))
+        mats.append((f"l{l}.up", (8192, 2048), "mlp"))
+        mats.append((f"l{l}.down", (2048, 8192), "mlp"))
+        for nm in ("ln1.w", "ln1.b", "ln2.w", "ln2.b"):
+            vecs.append((f"l{l}.{nm}", (2048,)))
+    vecs += [("lnf.w", (2048,)), ("lnf.b", (2048,))]
+    return mats, vecs
+
+
+def config5_params(torch, dev):
+    mats, vecs = config5_shapes()
+    g = torch.Generator(device=dev).manual_seed(6)
+    P = {}
+    for name, shape, _ in mats:
+        P[name] = torch.nn.Parameter(0.02 * torch.randn(shape, generator=g, device=dev))
+    for name, shape in vecs:
+        P[name] = torch.nn.Parameter(torch.ones(shape, device=dev) if name.endswith(".w")
+                                     else torch.zeros(shape, device=dev))
+    P["emb"] = torch.nn.Parameter(0.02 * torch.randn(32000, 2048, generator=g, device=dev))
+    return P
+
+
+def set_grads(torch, P, step, dev):
+    g = torch.Generator(device=dev).manual_seed(10_000 + step)
+    for p in P.values():
+        p.grad = 1e-3 * torch.randn(p.shape, generator=g, device=dev)
+
+
+def bench_optimizer(torch, ops, hip, dev, steps, cpu):
+    from pytorch_opt import Muon, Shampoo
+
+    mats, vecs = config5_shapes()
+    kind = {n: k for n, _, k in mats}
+    out = {}
+
+    def run(make_opt):
+        P = config5_params(torch, dev)
+        opt = make_opt(P)
+        total, per = 0.0, []
+        for t in range(steps):
+            set_grads(torch, P, t, dev)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            opt.step()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            per.append(dt)
+            total += dt
+        del P, opt
+        torch.cuda.empty_cache()
+        return total / steps, per
+
+    def make_muon(P):
+        routed = [P[n] for n, _, _ in mats]
+        rest = [P[n] for n, _ in vecs] + [P["emb"]]
+        return Muon([{"params": routed}, {"params": rest, "use_muon": False}], lr=0.02)
+
+    def make_shampoo(P):
+        attn = [P[n] for n, _, _ in mats if kind[n] == "attn"]
+        rest = [P[n] for n, _, _ in mats if kind[n] == "mlp"] + [P[n] for n, _ in vecs] + [P["emb"]]
+        return Shampoo([{"params": attn}, {"params": rest, "use_preconditioner": False, "lr": 3e-4}],
+                       max_preconditioner_dim=4096, precondition_frequency=20, graft="adagrad")
+
+    m_mean, _ = run(make_muon)
+    s_mean, s_per = run(make_shampoo)
+    refresh = [s_per[i] for i in range(steps) if i % 20 == 0]
+    plain = [s_per[i] for i in range(steps) if i % 20 != 0]
+    out["muon_step_ms"] = round(m_mean * 1e3, 2)
+    out["shampoo_step_ms"] = round(s_mean * 1e3, 2)
+    out["shampoo_refresh_step_ms"] = round(1e3 * sum(refresh) / max(len(refresh), 1), 1)
+    out["shampoo_plain_step_ms"] = round(1e3 * sum(plain) / max(len(plain), 1), 2)
+    out["muon_plus_shampoo_step_ms"] = round((m_mean + s_mean) * 1e3, 2)
+    out["muon_alg_tflops"] = round(sum(ns5_flops(*s) for _, s, _ in mats) / m_mean / 1e12, 2)
+    out["steps"] = steps
+    if cpu:
+        out["cpu"] = cpu_optimizer_estimate(torch, steps)
+        out["speedup_vs_cpu"] = round(out["cpu"]["muon_plus_shampoo_step_ms"] / out["muon_plus_shampoo_step_ms"], 1)
+    return out
+
+
+def cpu_optimizer_estimate(torch, steps):
+    """Per-step CPU time of the same two arms from a bounded sample of the
+    numpy oracle: one NS5 of each shape, one factor update + apply, one
+    fp64 eigendecomposition root (the reference's default 'auto'), one AdamW
+    pass over 2048x8192 — each scaled by its count per step."""
+    import numpy as np
+
+    from oracle import ops_oracle as oo
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(0)
+    sq = (1e-3 * rng.standard_normal((2048, 2048))).astype(np.float32)
+    wide = (1e-3 * rng.standard_normal((2048, 8192))).astype(np.float32)
+    t_ns_sq = timed(lambda: oo.ns5(sq))
+    t_ns_wide = timed(lambda: oo.ns5(wide))
+    L = (sq @ sq.T).astype(np.float32)
+    t_kron = timed(lambda: oo.kron_factor_update(L, L, sq, 0.999))
+    t_apply = timed(lambda: oo.precond_apply(L, sq, L))
+    t_root = timed(lambda: oo.inverse_root(L / np.float32(0.001), 4, damping=1e-8, method="auto"))
+    m = np.zeros_like(wide)
+    v = np.zeros_like(wide)
+    t_adamw = timed(lambda: oopt.adamw_step(wide, wide, m, v, 1, 3e-4))  # per 16.8M elements
+    per_elem = t_adamw / wide.size
+    emb_norms = 32000 * 2048 + 12 * 4 * 2048 + 2 * 2048
+    mlp = 24 * 2048 * 8192
+    muon = 48 * t_ns_sq + 24 * t_ns_wide + per_elem * emb_norms
+    plain = 48 * (t_kron + t_apply) + per_elem * (emb_norms + mlp)
+    refresh = plain + 96 * t_root
+    shampoo = (2 * refresh + (steps - 2) * plain) / steps
+    return {"muon_step_ms": round(muon * 1e3, 1), "shampoo_step_ms": round(shampoo * 1e3, 1),
+            "muon_plus_shampoo_step_ms": round((muon + shampoo) * 1e3, 1), "cores": blas_threads(), "kind": "port",
+            "sample": "numpy oracle: 1 NS5 2048², 1 NS5 2048x8192, 1 kron update + apply 2048², 1 fp64 eigh root "
+                      "2048, AdamW over 2048x8192; scaled by per-step counts (48, 24, 48, 96 per refresh, "
+                      "elements); Shampoo mean = (2 refresh + (steps-2) plain)/steps"}
+
+
+# ------------------------------------------------------------ main
 
 def main():
     ap = argparse.ArgumentParser()
@@ -88,6 +315,8 @@ def main():
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="headline only (no factors/roots/optimizer)")
+    ap.add_argument("--opt-steps", type=int, default=40)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -104,7 +333,8 @@ def main():
     hip = ops._NATIVE
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    inputs = [make_inputs(torch, b, r, c, s, dev) for b, r, c, s in SHAPES]
+    cpu = not args.no_cpu_baseline
+    inputs = [make_ns5_inputs(torch, b, r, c, s, dev) for b, r, c, s in SHAPES]
     torch.cuda.synchronize()
 
     def step():
@@ -113,7 +343,6 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-
     hip.prof_reset()
     hip.prof_enable(True)
     torch.cuda.synchronize()
@@ -128,32 +357,32 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     flops_step = sum(b * ns5_flops(r, c) for b, r, c, _ in SHAPES)
     value = flops_step / (ms_per_step / 1e3) / 1e12
-
     kinds = {}
     for kind in ("ns5_gram", "ns5_square", "ns5_update"):
         ms, launches = hip.prof_query(kind)
-        fl = args.steps * 5 * sum(b * kernel_flops(kind, r, c) for b, r, c, _ in SHAPES)
-        kinds[kind] = {"ms_total": ms, "launches": launches, "avg_ms": ms / max(launches, 1),
-                       "tflops": fl / (ms / 1e3) / 1e12 if ms > 0 else None}
+        fl = args.steps * 5 * sum(b * ns5_kernel_flops(kind, r, c) for b, r, c, _ in SHAPES)
+        kinds[kind] = {"ms_total": round(ms, 3), "launches": launches, "avg_ms": round(ms / max(launches, 1), 4),
+                       "alg_flops_per_launch": fl // max(launches, 1),
+                       "tflops": round(fl / (ms / 1e3) / 1e12, 2) if ms > 0 else None}
     dom = max(kinds, key=lambda k: kinds[k]["ms_total"])
     achieved = kinds[dom]["tflops"]
 
-    # single 4096x4096 matrix (the headline shape, unbatched)
     single = inputs[0][:1].contiguous()
     for _ in range(3):
         ops.newton_schulz_orthogonalize(single)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 10
     e0.record()
-    for _ in range(reps):
+    for _ in range(10):
         ops.newton_schulz_orthogonalize(single)
     e1.record()
     torch.cuda.synchronize()
-    single_ms = e0.elapsed_time(e1) / reps
+    single_ms = e0.elapsed_time(e1) / 10
     single_tflops = ns5_flops(4096, 4096) / (single_ms / 1e3) / 1e12
 
-    cpu = None if args.no_cpu_baseline else cpu_baseline(inputs)
+    cpu_line = cpu_baseline_ns5(inputs) if cpu else None
+    del inputs
+    torch.cuda.empty_cache()
 
     line = {
         "metric": "NS5 TFLOP/s (algorithmic, LAWN-41) on 32x4096^2 + 32x4096x11008 bf16, 5 iterations",
@@ -169,16 +398,18 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded N(0,1e-3) gradients folded into Nesterov momentum (beta 0.95, 3 steps)",
         "config": {"workload": "batched NS5 bf16: 32 x 4096x4096 + 32 x 4096x11008, 5 quintic iterations",
-                   "alg_flops_per_step": flops_step, "pct_bf16_mfma_peak": round(100 * value / BF16_PEAK_TFLOPS, 2),
-                   "peak_tflops": BF16_PEAK_TFLOPS},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2), "peak": BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": None},
-        "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                    for k, v in kinds.items()},
+                   "alg_flops_per_step": flops_step, "pct_bf16_mfma_peak": round(100 * value / PEAK["bf16"], 2)},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK["bf16"], "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK["bf16"], 4), "traffic": None},
+        "kernels": kinds,
         "single_4096": {"ms": round(single_ms, 3), "tflops": round(single_tflops, 2),
-                        "pct_bf16_mfma_peak": round(100 * single_tflops / BF16_PEAK_TFLOPS, 2)},
-        "cpu_baseline": cpu,
+                        "pct_bf16_mfma_peak": round(100 * single_tflops / PEAK["bf16"], 2)},
+        "cpu_baseline": cpu_line,
     }
+    if not args.no_extras:
+        line["factors"] = bench_factors(torch, ops, hip, dev, cpu)
+        line["roots"] = bench_roots(torch, hip, dev, cpu)
+        line["optimizer"] = bench_optimizer(torch, ops, hip, dev, args.opt_steps, cpu)
     print(json.dumps(line))
 
 

@@ -180,8 +180,17 @@ struct LdsPlan {
   static constexpr int WTM = Cfg::BM / Cfg::WM, WTN = Cfg::BN / Cfg::WN;
   static constexpr int STAGE = (Cfg::BM + Cfg::BN) * kRowBytes;
   static constexpr int WPA = (NW + kStages - 1) / kStages;  // waves per array in the epilogue
-  static constexpr int RPP = WTM < 64 ? WTM : 64;            // rows per epilogue pass
   static constexpr int SP = WTN + 1;
+  static constexpr int kLdsMax = 160 * 1024;
+  // rows per epilogue pass: at most 64, halved until the four arrays fit
+  static constexpr int pick_rpp() {
+    int r = WTM < 64 ? WTM : 64;
+    while (r > 16 && kStages * (STAGE > WPA * r * SP * (int)sizeof(S) ? STAGE : WPA * r * SP * (int)sizeof(S)) >
+                         kLdsMax)
+      r /= 2;
+    return r;
+  }
+  static constexpr int RPP = pick_rpp();
   static constexpr int EPI = WPA * RPP * SP * (int)sizeof(S);
   static constexpr int ARR = ((STAGE > EPI ? STAGE : EPI) + 15) / 16 * 16;
 };
@@ -205,6 +214,8 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0 && WTM % 16 == 0, "wave tile");
   static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
   static_assert(3 * IPW <= 63, "vmcnt range");
+  static_assert(Plan::RPP % MF::MN == 0 && WTM % Plan::RPP == 0, "epilogue passes");
+  static_assert(kStages * Plan::ARR <= Plan::kLdsMax, "LDS budget");
 
   if (g.guard != nullptr && *g.guard != 0) return;
 
