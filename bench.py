@@ -307,6 +307,61 @@ def cpu_optimizer_estimate(torch, steps):
                       "elements); Shampoo mean = (2 refresh + (steps-2) plain)/steps"}
 
 
+# ------------------------------------------------------------ HBM traffic
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ns5_bf16_traffic.json")
+COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written
+
+
+def traffic_probe(torch, ops, dev):
+    """One NS5 step of the headline workload and a 1 GiB device copy, for
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
+    inputs = [make_ns5_inputs(torch, b, r, c, s, dev) for b, r, c, s in SHAPES]
+    for G in inputs:
+        ops.newton_schulz_orthogonalize(G)
+    x = torch.ones(COPY_BYTES // 4, device=dev)
+    y = torch.empty_like(x)
+    y.copy_(x)
+    torch.cuda.synchronize()
+    print("traffic probe done", flush=True)
+
+
+def digest_traffic(fetch_csv, write_csv):
+    """Per-dispatch FETCH_SIZE / WRITE_SIZE (KiB) of the ns5_update kernel,
+    scaled by what the counters read for the 1 GiB copy."""
+    import csv
+
+    def per_kernel(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        upd = [float(r["Counter_Value"]) for r in rows if "EpiNsUpdate" in r["Kernel_Name"]
+               and "Tile<256" in r["Kernel_Name"].replace("TileILi256", "Tile<256")]
+        # the 1 GiB same-dtype copy runs as the runtime's copyBuffer blit
+        copy = [float(r["Counter_Value"]) for r in rows if "copyBuffer" in r["Kernel_Name"]]
+        return upd, copy
+
+    fu, fc = per_kernel(fetch_csv, "FETCH_SIZE")
+    wu, wc = per_kernel(write_csv, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (max(fc) * 1024.0)
+    w_scale = COPY_BYTES / (max(wc) * 1024.0)
+    fetch = sum(fu) / len(fu) * 1024.0 * f_scale
+    write = sum(wu) / len(wu) * 1024.0 * w_scale
+    out = {"kernel": "ns5_update", "launches": len(fu), "fetch_bytes_per_launch": int(fetch),
+           "write_bytes_per_launch": int(write), "traffic_bytes_per_launch": int(fetch + write),
+           "copy_fetch_kib": max(fc), "copy_write_kib": max(wc), "fetch_scale": round(f_scale, 4),
+           "write_scale": round(w_scale, 4)}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
 # ------------------------------------------------------------ main
 
 def main():
@@ -317,7 +372,13 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="headline only (no factors/roots/optimizer)")
     ap.add_argument("--opt-steps", type=int, default=40)
+    ap.add_argument("--traffic-probe", action="store_true", help="one NS5 step + 1 GiB copy, for PMC runs")
+    ap.add_argument("--digest-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="write the ns5_update HBM traffic summary from two PMC runs")
     args = ap.parse_args()
+    if args.digest_traffic:
+        digest_traffic(*args.digest_traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(matrices shard by whole matrices across GPUs; see the design notes).", file=sys.stderr)
@@ -334,6 +395,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cpu = not args.no_cpu_baseline
+    if args.traffic_probe:
+        traffic_probe(torch, ops, dev)
+        return
     inputs = [make_ns5_inputs(torch, b, r, c, s, dev) for b, r, c, s in SHAPES]
     torch.cuda.synchronize()
 
@@ -400,7 +464,7 @@ def main():
         "config": {"workload": "batched NS5 bf16: 32 x 4096x4096 + 32 x 4096x11008, 5 quintic iterations",
                    "alg_flops_per_step": flops_step, "pct_bf16_mfma_peak": round(100 * value / PEAK["bf16"], 2)},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK["bf16"], 4), "traffic": None},
+                     "frac": round(achieved / PEAK["bf16"], 4), "traffic": load_traffic()},
         "kernels": kinds,
         "single_4096": {"ms": round(single_ms, 3), "tflops": round(single_tflops, 2),
                         "pct_bf16_mfma_peak": round(100 * single_tflops / PEAK["bf16"], 2)},
