@@ -201,7 +201,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   typedef typename MF::cvec_t cvec_t;
   typedef typename Epi::S S;
   typedef LdsPlan<T, Cfg, S> Plan;
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT, NW = Plan::NW;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Plan::NW;
   constexpr int BK = kRowBytes / (int)sizeof(T);   // elements per K tile
   constexpr int VEC = 16 / (int)sizeof(T);         // elements per 16-byte chunk
   constexpr int WTM = Plan::WTM, WTN = Plan::WTN;
@@ -323,11 +323,21 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // functor is a run of up to 8 consecutive elements of one output row.
   // Each wave owns a private slice (RPP rows of its WTM x WTN sub-tile at a
   // time), so no cross-wave synchronisation is needed:
-  //   1. the wave writes RPP rows of raw accumulators to its slice;
+  //   1. the functor's global reads for all of this lane's direct runs are
+  //      issued (epi.load), then the wave writes RPP rows of raw
+  //      accumulators to its slice while they are in flight;
   //   2. direct pass: runs along output rows (i, j..j+7) -> epi.put, which
   //      hands back the value the transposed pass should see;
   //   3. transposed pass (mirror of a symmetric tile, or the functor's
-  //      transposed copy): runs along (j, i..i+7) -> epi.put_t.
+  //      transposed copy): reads for all runs (epi.load_t), then runs along
+  //      (j, i..i+7) -> epi.put_t.
+  // Reading before writing keeps one memory latency per pass instead of
+  // one per run: a functor may read and write the same array (X' = a·X + v
+  // in place), so the compiler cannot hoist a run's read above the
+  // previous run's store by itself. Each run reads and writes only its own
+  // elements, and the direct and transposed runs of one tile cover
+  // disjoint positions, so the early reads see the values from before the
+  // launch.
   // In symmetric (UPPER) products the value for (i, j), i <= j, is stored
   // at (i, j) by its own direct pass and at (j, i) by its transposed pass;
   // on diagonal tiles positions below the diagonal are skipped by the
@@ -339,11 +349,30 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const bool need_t = UPPER || epi.has_t();
   const int wr0 = row0 + wm * WTM, wc0 = col0 + wn * WTN;  // sub-tile origin
   const int nrem = g.N - wc0;
+  // direct runs: 8 lanes cover 64 consecutive columns of one row
+  constexpr int RUNS = WTN / 8;  // 8-element runs per row
+  constexpr int LGD = RUNS < 8 ? RUNS : 8;
+  constexpr int RPB = 64 / LGD;
+  constexpr int CBLK = RUNS / LGD;
+  constexpr int ITEMS = ((RPP + RPB - 1) / RPB) * CBLK;  // direct runs per lane
+  // transposed runs: 8 lanes share a column c and cover 64 consecutive rows
+  constexpr int CBT = WTN / 8;
+  constexpr int ITEMS_T = ((RPP / 8 + 7) / 8) * CBT;
 #pragma unroll
   for (int hp = 0; hp < WTM / RPP; ++hp) {
     const int pr0 = wr0 + hp * RPP;  // first output row of this pass
     if (pr0 >= g.M || nrem <= 0) break;
     const int rows = min(RPP, g.M - pr0);
+    typename Epi::Pre pre[ITEMS];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int r = (it / CBLK) * RPB + lane / LGD;
+      const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
+      const int i = pr0 + r, j0 = wc0 + c;
+      const int n = min(8, nrem - c);
+      const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
+      if (r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);
+    }
 #pragma unroll
     for (int fm = hp * (RPP / MF::MN); fm < (hp + 1) * (RPP / MF::MN); ++fm)
 #pragma unroll
@@ -356,24 +385,18 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
         }
     __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
     __builtin_amdgcn_wave_barrier();
-    // direct pass: 8 lanes cover 64 consecutive columns of one row
-    constexpr int RUNS = WTN / 8;                  // 8-element runs per row
-    constexpr int LGD = RUNS < 8 ? RUNS : 8;
-    constexpr int RPB = 64 / LGD;
-    constexpr int CBLK = RUNS / LGD;
-    for (int t = lane; t < ((RPP + RPB - 1) / RPB) * CBLK * 64; t += 64) {
-      const int blk = t >> 6, w = t & 63;
-      const int r = (blk / CBLK) * RPB + w / LGD;
-      const int c = ((blk % CBLK) * LGD + w % LGD) * 8;
-      if (r >= rows || c >= nrem) continue;
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int r = (it / CBLK) * RPB + lane / LGD;
+      const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
       const int i = pr0 + r, j0 = wc0 + c;
       const int n = min(8, nrem - c);
-      const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
-      if (kbeg >= n) continue;
+      const int kbeg = diag ? max(0, i - j0) : 0;
+      if (!(r < rows && c < nrem && kbeg < n)) continue;
       S v[8], vo[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
-      epi.put(b, i, j0, v, kbeg, n, vo);
+      epi.put(b, i, j0, v, kbeg, n, pre[it], vo);
       if (need_t) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];
@@ -382,22 +405,29 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     if (need_t) {
       __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
       __builtin_amdgcn_wave_barrier();
-      // transposed pass: output row j = wc0 + c, columns i = pr0 + r..r+7;
-      // 8 lanes share c and cover 64 consecutive i
-      const int rgroups = (rows + 7) / 8;
-      for (int t = lane; t < ((rgroups + 7) / 8) * WTN * 8; t += 64) {
-        const int blk = t >> 6, w = t & 63;
-        const int c = (blk % (WTN / 8)) * 8 + w / 8;
-        const int r = ((blk / (WTN / 8)) * 8 + w % 8) * 8;
-        if (c >= nrem || r >= rows) continue;
+      // output row j = wc0 + c, columns i = pr0 + r..r+7
+      typename Epi::PreT pret[ITEMS_T];
+#pragma unroll
+      for (int it = 0; it < ITEMS_T; ++it) {
+        const int c = (it % CBT) * 8 + lane / 8;
+        const int r = ((it / CBT) * 8 + lane % 8) * 8;
         const int j = wc0 + c, i0 = pr0 + r;
         int n = min(8, rows - r);
         if (diag) n = min(n, j - i0);  // strictly below the diagonal
-        if (n <= 0) continue;
+        if (c < nrem && r < rows && n > 0) epi.load_t(b, j, i0, n, pret[it]);
+      }
+#pragma unroll
+      for (int it = 0; it < ITEMS_T; ++it) {
+        const int c = (it % CBT) * 8 + lane / 8;
+        const int r = ((it / CBT) * 8 + lane % 8) * 8;
+        const int j = wc0 + c, i0 = pr0 + r;
+        int n = min(8, rows - r);
+        if (diag) n = min(n, j - i0);
+        if (!(c < nrem && r < rows && n > 0)) continue;
         S v[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(r + k) * SP + c] : S(0);
-        epi.put_t(b, j, i0, v, n);
+        epi.put_t(b, j, i0, v, n, pret[it]);
       }
     }
     __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
@@ -482,15 +512,21 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
 
 // ------------------------------------------------------------- epilogues
 // Functor interface (S = staging/accumulation type):
-//   put(b, i, j0, v[8], kbeg, n, vo[8])  output row i, columns j0+k for
-//       k in [kbeg, n); vo receives what the transposed pass should see;
-//   put_t(b, j, i0, v[8], n)             output row j, columns i0+k, k < n
+//   Pre, PreT                            what a direct / transposed run
+//       reads from global memory before it writes (empty if nothing);
+//   load(b, i, j0, kbeg, n, Pre&)        issue those reads for a direct run;
+//   put(b, i, j0, v[8], kbeg, n, pre, vo[8])  output row i, columns j0+k
+//       for k in [kbeg, n); vo receives what the transposed pass should see;
+//   load_t(b, j, i0, n, PreT&)           reads for a transposed run;
+//   put_t(b, j, i0, v[8], n, pre_t)      output row j, columns i0+k, k < n
 //       (the mirror of a symmetric product, or a transposed copy);
 //   has_t()                              whether put_t is needed outside
 //       symmetric products;
 //   finish(b)                            once per thread at the end.
 // j0 and i0 are multiples of 8; `vec` (set by the host when the row pitch,
 // batch stride and base allow) enables 16-byte accesses for full runs.
+
+struct NoPre {};
 
 template <typename T>
 __device__ __forceinline__ bool full_run(bool vec, int kbeg, int n) {
@@ -549,6 +585,58 @@ __device__ __forceinline__ void st8(T* p, const S* in, int kbeg, int n, bool vec
   }
 }
 
+// Eight elements of T held in their storage format between the read and
+// the use, so a pending run costs 4 (bf16), 8 (fp32) or 16 (fp64) VGPRs.
+template <typename T>
+struct Raw8 {
+  uint4 w[sizeof(T) / 2];
+};
+
+// Early read of a full run (16-byte loads straight into r). Partial runs
+// (matrix edges, diagonal tiles) are read at use time by ld8_use instead:
+// filling single elements of r here would make the compiler split the
+// full-run registers, and so wait for the loads, right after issuing them.
+template <typename T>
+__device__ __forceinline__ void ld8_pre(const T* p, Raw8<T>& r, int kbeg, int n, bool vec) {
+  if (full_run<T>(vec, kbeg, n)) {
+#pragma unroll
+    for (int q = 0; q < (int)(sizeof(T) / 2); ++q) r.w[q] = reinterpret_cast<const uint4*>(p)[q];
+  }
+}
+
+// out[k] = p[k] for k in [kbeg, n), from r if ld8_pre read the run. The
+// unpacking works on whole 32-bit words (a bf16 is the high half of the
+// float with the same value) so the registers stay whole until here.
+template <typename T, typename S>
+__device__ __forceinline__ void ld8_use(const T* p, const Raw8<T>& r, S* out, int kbeg, int n, bool vec) {
+  if (full_run<T>(vec, kbeg, n)) {
+    if constexpr (sizeof(T) == 2) {
+      const unsigned w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        out[2 * q] = static_cast<S>(__uint_as_float(w[q] << 16));
+        out[2 * q + 1] = static_cast<S>(__uint_as_float(w[q] & 0xffff0000u));
+      }
+    } else if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        out[4 * q] = static_cast<S>(__uint_as_float(r.w[q].x));
+        out[4 * q + 1] = static_cast<S>(__uint_as_float(r.w[q].y));
+        out[4 * q + 2] = static_cast<S>(__uint_as_float(r.w[q].z));
+        out[4 * q + 3] = static_cast<S>(__uint_as_float(r.w[q].w));
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        out[2 * q] = static_cast<S>(__hiloint2double((int)r.w[q].y, (int)r.w[q].x));
+        out[2 * q + 1] = static_cast<S>(__hiloint2double((int)r.w[q].w, (int)r.w[q].z));
+      }
+    }
+  } else {
+    for (int k = kbeg; k < n; ++k) out[k] = static_cast<S>(to_f(p[k]));
+  }
+}
+
 // Host-side check that a [.., ld] buffer allows 16-byte runs of 8 elements.
 template <typename T>
 inline bool vec_ok(const void* p, int64_t ld, int64_t sb) {
@@ -562,13 +650,17 @@ struct EpiStore {
   TO* dst;
   int64_t ld, sd;
   bool vec;
+  typedef NoPre Pre;
+  typedef NoPre PreT;
   __device__ __forceinline__ bool has_t() const { return false; }
-  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, S* vo) const {
+  __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
+  __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre&, S* vo) const {
     st8<TO, S>(dst + (int64_t)b * sd + (int64_t)i * ld + j0, v, kbeg, n, vec);
 #pragma unroll
     for (int k = 0; k < 8; ++k) vo[k] = v[k];
   }
-  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n) const {
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT&) const {
     st8<TO, S>(dst + (int64_t)b * sd + (int64_t)j * ld + i0, v, 0, n, vec);
   }
   __device__ __forceinline__ void finish(int) const {}
@@ -582,12 +674,20 @@ struct EpiBlend {
   int64_t ld, sd;
   A beta, alpha;
   bool vec;
+  typedef Raw8<TO> Pre;
+  typedef Raw8<TO> PreT;
   __device__ __forceinline__ bool has_t() const { return false; }
-  __device__ __forceinline__ void blend(TO* p, const S* v, int kbeg, int n) const {
+  __device__ __forceinline__ void load(int b, int i, int j0, int kbeg, int n, Pre& p) const {
+    if (beta != A(0)) ld8_pre<TO>(dst + (int64_t)b * sd + (int64_t)i * ld + j0, p, kbeg, n, vec);
+  }
+  __device__ __forceinline__ void load_t(int b, int j, int i0, int n, PreT& p) const {
+    if (beta != A(0)) ld8_pre<TO>(dst + (int64_t)b * sd + (int64_t)j * ld + i0, p, 0, n, vec);
+  }
+  __device__ __forceinline__ void blend(TO* p, const S* v, int kbeg, int n, const Raw8<TO>& raw) const {
     S r[8];
     if (beta != A(0)) {
       S old[8];
-      ld8<TO, S>(p, old, kbeg, n, vec);
+      ld8_use<TO, S>(p, raw, old, kbeg, n, vec);
 #pragma unroll
       for (int k = 0; k < 8; ++k) r[k] = beta * old[k] + alpha * v[k];
     } else {
@@ -596,13 +696,14 @@ struct EpiBlend {
     }
     st8<TO, S>(p, r, kbeg, n, vec);
   }
-  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, S* vo) const {
-    blend(dst + (int64_t)b * sd + (int64_t)i * ld + j0, v, kbeg, n);
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre& pre,
+                                      S* vo) const {
+    blend(dst + (int64_t)b * sd + (int64_t)i * ld + j0, v, kbeg, n, pre);
 #pragma unroll
     for (int k = 0; k < 8; ++k) vo[k] = v[k];
   }
-  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n) const {
-    blend(dst + (int64_t)b * sd + (int64_t)j * ld + i0, v, 0, n);
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT& pre) const {
+    blend(dst + (int64_t)b * sd + (int64_t)j * ld + i0, v, 0, n, pre);
   }
   __device__ __forceinline__ void finish(int) const {}
 };

@@ -8,10 +8,13 @@
 //   undo the transpose; cast back.
 //
 // Per iteration three MFMA launches, each with a fused epilogue:
-//   1. A = X·Xᵀ              symmetric: upper tiles only, mirrored store
-//   2. B = b·A + c·(A·A)     symmetric: upper tiles only, mirrored store
-//   3. X' = a·X + B·X        full; writes X' and X'ᵀ (Xᵀ is the K-major
-//                            operand the next B·X needs)
+//   1. A = X·Xᵀ                    symmetric: upper tiles only, mirrored store
+//   2. B' = a·I + b·A + c·(A·A)    symmetric: upper tiles only, mirrored store
+//   3. X' = B'·X  (= a·X + B·X)    full; writes X' and X'ᵀ (Xᵀ is the
+//                                  K-major operand the next product needs)
+// Folding a·X into the product as a·I on the diagonal of B' spares the
+// update a read of X; the extra rounding is that of one bf16 store of
+// a + B_ii, the same size as the rounding of a·X itself in a bf16 chain.
 // All three are "NT" products over K-contiguous rows. bf16 inputs keep
 // X, A, B in bf16 between launches with fp32 accumulation; fp32 and fp64
 // inputs stay in their own precision throughout.
@@ -35,51 +38,57 @@ __global__ void ns_scale_kernel(const double* __restrict__ partial, int nblk, do
   scale[b] = A(1) / (nrm + static_cast<A>(eps));
 }
 
-// B = b·A + c·v  (A is symmetric, so the mirror takes the same value)
+// B' = a·I + b·A + c·v  (symmetric, so the mirror takes the same value)
 template <typename T, typename A>
 struct EpiNsSq {
   typedef A S;
   const T* Asrc;
   T* dst;
   int64_t ld, sd;
-  A bc, cc;
+  A ac, bc, cc;
   bool vec;
+  typedef Raw8<T> Pre;
+  typedef NoPre PreT;
   __device__ __forceinline__ bool has_t() const { return false; }
-  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, S* vo) const {
+  __device__ __forceinline__ void load(int b, int i, int j0, int kbeg, int n, Pre& p) const {
+    ld8_pre<T>(Asrc + (int64_t)b * sd + (int64_t)i * ld + j0, p, kbeg, n, vec);
+  }
+  __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre& pre,
+                                      S* vo) const {
     const int64_t o = (int64_t)b * sd + (int64_t)i * ld + j0;
     S a[8];
-    ld8<T, S>(Asrc + o, a, kbeg, n, vec);
+    ld8_use<T, S>(Asrc + o, pre, a, kbeg, n, vec);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) vo[k] = bc * a[k] + cc * v[k];
+    for (int k = 0; k < 8; ++k) vo[k] = bc * a[k] + cc * v[k] + (i == j0 + k ? ac : A(0));
     st8<T, S>(dst + o, vo, kbeg, n, vec);
   }
-  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n) const {
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT&) const {
     st8<T, S>(dst + (int64_t)b * sd + (int64_t)j * ld + i0, v, 0, n, vec);
   }
   __device__ __forceinline__ void finish(int) const {}
 };
 
-// X' = a·X + v, stored to dst (row-major) and/or dstT (transposed copy).
+// X' = v, stored to dst (row-major) and/or dstT (transposed copy).
 template <typename T, typename A>
 struct EpiNsUpdate {
   typedef A S;
-  const T* xsrc;
-  int64_t ld_x, s_x;
   T* dst;
   int64_t ld_d, s_d;
   T* dstT;
   int64_t ld_t, s_t;
-  A ac;
-  bool vec_x, vec_d, vec_t;
+  bool vec_d, vec_t;
+  typedef NoPre Pre;
+  typedef NoPre PreT;
   __device__ __forceinline__ bool has_t() const { return dstT != nullptr; }
-  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, S* vo) const {
-    S x[8];
-    ld8<T, S>(xsrc + (int64_t)b * s_x + (int64_t)i * ld_x + j0, x, kbeg, n, vec_x);
+  __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
+  __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre&, S* vo) const {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) vo[k] = ac * x[k] + v[k];
-    if (dst) st8<T, S>(dst + (int64_t)b * s_d + (int64_t)i * ld_d + j0, vo, kbeg, n, vec_d);
+    for (int k = 0; k < 8; ++k) vo[k] = v[k];
+    if (dst) st8<T, S>(dst + (int64_t)b * s_d + (int64_t)i * ld_d + j0, v, kbeg, n, vec_d);
   }
-  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n) const {
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT&) const {
     st8<T, S>(dstT + (int64_t)b * s_t + (int64_t)j * ld_t + i0, v, 0, n, vec_t);
   }
   __device__ __forceinline__ void finish(int) const {}
@@ -161,18 +170,17 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
       EpiStore<T, A> e{Ab, ldm, m * ldm, vec_ok<T>(Ab, ldm, m * ldm)};
       if (launch_gemm<T, true>(g, e, nb, stream, "ns5_gram")) return -1;
     }
-    // 2. B = b·A + c·A·A
+    // 2. B' = a·I + b·A + c·A·A
     {
       GemmArgs g{Ab, ldm, m * ldm, Ab, ldm, m * ldm, (int)m, (int)m, (int)ldm, 0, 0, nullptr};
-      EpiNsSq<T, A> e{Ab, Bb, ldm, m * ldm, static_cast<A>(b), static_cast<A>(c),
+      EpiNsSq<T, A> e{Ab, Bb, ldm, m * ldm, static_cast<A>(a), static_cast<A>(b), static_cast<A>(c),
                       vec_ok<T>(Ab, ldm, m * ldm) && vec_ok<T>(Bb, ldm, m * ldm)};
       if (launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
     }
-    // 3. X' = a·X + B·X   (B·X as B·(Xᵀ)ᵀ over the stored transpose)
+    // 3. X' = B'·X   (as B'·(Xᵀ)ᵀ over the stored transpose)
     {
       GemmArgs g{Bb, ldm, m * ldm, XT[cur], ldm, n * ldm, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
       EpiNsUpdate<T, A> e{};
-      e.xsrc = Xb; e.ld_x = ldn; e.s_x = m * ldn; e.ac = static_cast<A>(a);
       if (!last) {
         e.dst = Xb; e.ld_d = ldn; e.s_d = m * ldn;
         e.dstT = XT[cur ^ 1]; e.ld_t = ldm; e.s_t = n * ldm;
@@ -183,7 +191,6 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
         e.dst = nullptr;
         e.dstT = out; e.ld_t = cols; e.s_t = sG;
       }
-      e.vec_x = vec_ok<T>(e.xsrc, e.ld_x, e.s_x);
       e.vec_d = e.dst && vec_ok<T>(e.dst, e.ld_d, e.s_d);
       e.vec_t = e.dstT && vec_ok<T>(e.dstT, e.ld_t, e.s_t);
       if (launch_gemm<T, false>(g, e, nb, stream, "ns5_update")) return -1;

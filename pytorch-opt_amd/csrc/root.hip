@@ -140,7 +140,11 @@ struct EpiMk {
   typename Bits<R>::U* err;
   typename Bits<R>::U mx;
   bool vec;
+  typedef NoPre Pre;
+  typedef NoPre PreT;
   __device__ __forceinline__ bool has_t() const { return false; }
+  __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
+  __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
   // Row `row`, columns c0+k for k in [kbeg, n).
   __device__ __forceinline__ void run(int b, int row, int c0, const R* v, int kbeg, int n) {
     const int64_t o = (int64_t)b * sb + (int64_t)row * ld + c0;
@@ -161,12 +165,14 @@ struct EpiMk {
     st8<R, R>(Mk + o, v, kbeg, n, vec);
     st8<R, R>(Mi + o, mi, kbeg, n, vec);
   }
-  __device__ __forceinline__ void put(int b, int i, int j0, const R* v, int kbeg, int n, R* vo) {
+  __device__ __forceinline__ void put(int b, int i, int j0, const R* v, int kbeg, int n, const Pre&, R* vo) {
     run(b, i, j0, v, kbeg, n);
 #pragma unroll
     for (int k = 0; k < 8; ++k) vo[k] = v[k];
   }
-  __device__ __forceinline__ void put_t(int b, int j, int i0, const R* v, int n) { run(b, j, i0, v, 0, n); }
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const R* v, int n, const PreT&) {
+    run(b, j, i0, v, 0, n);
+  }
   __device__ __forceinline__ void finish(int) {
     for (int off = 32; off > 0; off >>= 1) {
       typename Bits<R>::U o = __shfl_xor(mx, off, 64);
