@@ -152,6 +152,18 @@ constexpr int kRowBytes = 64;
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 2) & 3) ^ (r & 2); }
 
+// "QN" operand layout (bf16 only): Q is stored [K][N], N contiguous, the
+// natural layout of X in X' = B·X, so no transposed copy of X is needed.
+// A stage then holds BK rows of BN elements (BN*2 bytes) for Q, and the
+// MFMA B fragments come from transposing LDS reads (ds_read_b64_tr_b16).
+// Within each 16-lane group, lane s addresses 4 elements at row k0 + s/4,
+// column n0 + 4*(s%4); lane s then receives column n0 + s of rows
+// k0..k0+3. 16-byte chunk c of Q row r lives at physical chunk
+// c ^ (4 * (r % 4)): the four rows of one read land in distinct banks.
+__device__ __forceinline__ int swzq(int r) { return 4 * (r & 3); }
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
 // s_waitcnt with only the vector-memory counter constrained (gfx9 layout:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
 #define PTO_VMCNT(n) ((((n) & 0xF) | ((((n) >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8)))
@@ -195,7 +207,7 @@ struct LdsPlan {
   static constexpr int ARR = ((STAGE > EPI ? STAGE : EPI) + 15) / 16 * 16;
 };
 
-template <typename T, class Cfg, bool UPPER, class Epi>
+template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false>
 __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   typedef Mfma<T> MF;
   typedef typename MF::cvec_t cvec_t;
@@ -210,12 +222,16 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   constexpr int NRG = KSPAN / VEC;                 // 16-byte fragment reads per tile
   constexpr int IPR = VEC / MF::KPL;               // MFMAs per 16-byte read
   constexpr int IPW = (BM + BN) / 16 / NW;         // DMA instructions per wave per tile
+  constexpr int QRB = QN ? BN * (int)sizeof(T) : kRowBytes;  // bytes per Q row in LDS
+  constexpr int CPR = QRB / 16;                    // 16-byte chunks per Q row
   static_assert((BM + BN) % (16 * NW) == 0 && IPW >= 1, "DMA split");
   static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0 && WTM % 16 == 0, "wave tile");
   static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
   static_assert(3 * IPW <= 63, "vmcnt range");
   static_assert(Plan::RPP % MF::MN == 0 && WTM % Plan::RPP == 0, "epilogue passes");
   static_assert(kStages * Plan::ARR <= Plan::kLdsMax, "LDS budget");
+  static_assert(!QN || (sizeof(T) == 2 && !UPPER && CPR >= 16 && 1024 % QRB == 0 && (BM * kRowBytes) % 1024 == 0),
+                "QN layout: bf16 full products, Q rows of 256 bytes or more");
 
   if (g.guard != nullptr && *g.guard != 0) return;
 
@@ -234,36 +250,43 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   decode_tile<UPPER>(logical - b * ntile, g.tiles_m, g.tiles_n, ti, tj);
   const int row0 = ti * BM, col0 = tj * BN;
 
-  // Per-thread DMA sources: instruction q of this wave fills stage rows
-  // R0 = 16*(wave*IPW + q) .. +15 (P rows first, then Q rows); this lane
-  // supplies row R0 + lane/4, physical chunk lane%4, i.e. logical chunk
-  // (lane%4) ^ swz(row). Rows past M (N) re-read the last valid row.
+  // Per-thread DMA sources: instruction q of this wave fills the 1 KiB of
+  // the stage at R0*64 bytes, R0 = 16*(wave*IPW + q) (P rows first, then
+  // Q); lane L supplies bytes 16L..16L+15 of it. In the K-contiguous
+  // layout that is row R0 + L/4, physical chunk L%4, i.e. logical chunk
+  // (L%4) ^ swz(row); rows past M (N) re-read the last valid row. In the
+  // QN layout a Q lane supplies row rq = byte offset / QRB, physical chunk
+  // L % CPR, logical chunk (L % CPR) ^ swzq(rq); columns past the row
+  // pitch re-read its last chunk.
   const T* src[IPW];
+  int64_t step[IPW];  // elements between consecutive K tiles
   int dst_off[IPW];
 #pragma unroll
   for (int q = 0; q < IPW; ++q) {
     const int R0 = 16 * (wave * IPW + q), r = R0 + (lane >> 2);
     const int chunk = (lane & 3) ^ swz(r);
-    const T* base;
-    int64_t ld;
-    int gr;
     if (R0 < BM) {
-      base = static_cast<const T*>(g.P) + (int64_t)b * g.sP;
-      ld = g.ldp;
-      gr = min(row0 + r, max(g.M - 1, 0));
+      const int gr = min(row0 + r, max(g.M - 1, 0));
+      src[q] = static_cast<const T*>(g.P) + (int64_t)b * g.sP + (int64_t)gr * g.ldp + chunk * VEC;
+      step[q] = BK;
+    } else if (!QN) {
+      const int gr = min(col0 + (r - BM), max(g.N - 1, 0));
+      src[q] = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)gr * g.ldq + chunk * VEC;
+      step[q] = BK;
     } else {
-      base = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ;
-      ld = g.ldq;
-      gr = min(col0 + (r - BM), max(g.N - 1, 0));
+      const int rq = (R0 - BM) * kRowBytes / QRB + lane / CPR;
+      const int c = (lane % CPR) ^ swzq(rq);
+      const int64_t col = min((int64_t)col0 + c * VEC, g.ldq - VEC);
+      src[q] = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)rq * g.ldq + col;
+      step[q] = (int64_t)BK * g.ldq;
     }
-    src[q] = base + (int64_t)gr * ld + chunk * VEC;
     dst_off[q] = R0 * kRowBytes;
   }
   auto issue = [&](int kt, char* stage) {
 #pragma unroll
     for (int q = 0; q < IPW; ++q)
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(src[q] + (int64_t)kt * BK), (lds_void_t*)(stage + dst_off[q]),
-                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(src[q] + (int64_t)kt * step[q]),
+                                       (lds_void_t*)(stage + dst_off[q]), 16, 0, 0);
   };
 
   cvec_t acc[FM][FN];
@@ -276,9 +299,20 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 
   const int lr = lane % MF::MN, lg = lane / MF::MN;
   const int sw = swz(lr);  // rows of every fragment are lr mod 16
+  // QN: byte offset of this lane's transposing read for fragment fn, MFMA
+  // step 0, first half; step rg and the second half (k + 4) add whole rows,
+  // which keep the row's swizzle (row % 4 = (lane % 16) / 4).
+  int qoff[FN];
+  if constexpr (QN) {
+    const int li = lane & 15, qr = 16 * lg + (li >> 2);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int col = wn * WTN + fn * MF::MN + 16 * ((lane >> 4) & 1) + 4 * (li & 3);
+      qoff[fn] = qr * QRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
+    }
+  }
   auto compute = [&](const char* stage) {
     const char* Pw = stage + (wm * WTM + lr) * kRowBytes;
-    const char* Qw = stage + (BM + wn * WTN + lr) * kRowBytes;
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       const int off = ((lg * NRG + rg) ^ sw) * 16;
@@ -286,9 +320,22 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
         a[fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
+      if constexpr (QN) {
+        // lanes of k-half lg, step rg: k = 16*lg + 8*rg + 0..7
+        const char* Qs = stage + BM * kRowBytes + 8 * rg * QRB;
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
-        bq[fn] = *reinterpret_cast<const uint4*>(Qw + fn * MF::MN * kRowBytes + off);
+        for (int fn = 0; fn < FN; ++fn) {
+          v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(Qs + qoff[fn]));
+          v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(Qs + qoff[fn] + 4 * QRB));
+          uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          bq[fn] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+      } else {
+        const char* Qw = stage + (BM + wn * WTN + lr) * kRowBytes;
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          bq[fn] = *reinterpret_cast<const uint4*>(Qw + fn * MF::MN * kRowBytes + off);
+      }
 #pragma unroll
       for (int ii = 0; ii < IPR; ++ii)
 #pragma unroll
@@ -466,7 +513,7 @@ struct TileSet<double> {
   typedef small sym_small;
 };
 
-template <typename T, class Cfg, bool UPPER, class Epi>
+template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false>
 int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
   g.tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
   g.tiles_n = (g.N + Cfg::BN - 1) / Cfg::BN;
@@ -474,7 +521,7 @@ int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, c
   if (tiles == 0 || batch == 0) return 0;
   PTO_REQUIRE(tiles < (1ll << 31) && batch < 65536, std::string(name) + ": grid too large");
   ProfScope ps(name, stream);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi>), dim3((unsigned)tiles, (unsigned)batch),
+  hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi, QN>), dim3((unsigned)tiles, (unsigned)batch),
                      dim3(Cfg::NT), 0, stream, g, epi);
   PTO_LAUNCHED(name);
   return 0;
@@ -508,6 +555,24 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
   int64_t big_tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
   if (big_tiles >= 512) return launch_gemm_cfg<T, Big, UPPER, Epi>(g, epi, batch, stream, name);
   return launch_gemm_cfg<T, Small, UPPER, Epi>(g, epi, batch, stream, name);
+}
+
+// C[b](i,j) = sum_k P[b](i,k) * Q[b](k,j) with Q stored [K][N] (row pitch
+// ldq, N contiguous), bf16 only. Q must hold K rows of ldq elements, and
+// its rows past the true contraction length must be zero (as the pad
+// columns of P are).
+template <class Epi>
+int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
+  typedef typename TileSet<bf16>::big Big;
+  typedef typename TileSet<bf16>::small Small;
+  PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
+  PTO_REQUIRE(g.K % Big::BK == 0 && g.K % Small::BK == 0, std::string(name) + ": K not padded");
+  PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 &&
+                  (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
+              std::string(name) + ": operands not 16-byte aligned");
+  int64_t big_tiles = (int64_t)((g.M + Big::BM - 1) / Big::BM) * ((g.N + Big::BN - 1) / Big::BN) * batch;
+  if (big_tiles >= 512) return launch_gemm_cfg<bf16, Big, false, Epi, true>(g, epi, batch, stream, name);
+  return launch_gemm_cfg<bf16, Small, false, Epi, true>(g, epi, batch, stream, name);
 }
 
 // ------------------------------------------------------------- epilogues

@@ -100,6 +100,14 @@ struct NsLayout {
   bool transposed;
 };
 
+// bf16 updates read X itself as the [K][N] operand of X' = B'·X (QN
+// layout), ping-ponging between two X buffers with ldm rows whose pad rows
+// are zero. fp32 and fp64 keep one X and a ping-pong pair of stored Xᵀ.
+template <typename T>
+constexpr bool ns5_qn() {
+  return sizeof(T) == 2;
+}
+
 template <typename T>
 size_t ns5_ws_bytes_t(int64_t batch, int64_t rows, int64_t cols) {
   int64_t m = std::min(rows, cols), n = std::max(rows, cols);
@@ -112,9 +120,14 @@ size_t ns5_ws_bytes_t(int64_t batch, int64_t rows, int64_t cols) {
   add(sizeof(A) * batch);                      // scales
   add(e * batch * m * ldm);                    // A
   add(e * batch * m * ldm);                    // B
-  add(e * batch * m * ldn);                    // X
-  add(e * batch * n * ldm);                    // Xᵀ ping
-  add(e * batch * n * ldm);                    // Xᵀ pong
+  if (ns5_qn<T>()) {
+    add(e * batch * ldm * ldn);                // X ping
+    add(e * batch * ldm * ldn);                // X pong
+  } else {
+    add(e * batch * m * ldn);                  // X
+    add(e * batch * n * ldm);                  // Xᵀ ping
+    add(e * batch * n * ldm);                  // Xᵀ pong
+  }
   return bytes + 256;
 }
 
@@ -128,13 +141,23 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
   PTO_REQUIRE(m <= INT32_MAX && n <= INT32_MAX && batch <= 65535, "newton_schulz_orthogonalize: shape too large");
   if (batch == 0 || rows == 0 || cols == 0) return 0;
 
+  constexpr bool QN = ns5_qn<T>();
   Carver cv(ws, ws_bytes);
   double* partial = cv.take<double>(kRedBlocks * batch);
   A* scale = cv.take<A>(batch);
   T* Ab = cv.take<T>(batch * m * ldm);
   T* Bb = cv.take<T>(batch * m * ldm);
-  T* Xb = cv.take<T>(batch * m * ldn);
-  T* XT[2] = {cv.take<T>(batch * n * ldm), cv.take<T>(batch * n * ldm)};
+  const int64_t sX = QN ? ldm * ldn : m * ldn;  // batch stride of X
+  T* X[2];
+  T* XT[2] = {nullptr, nullptr};
+  X[0] = cv.take<T>(batch * sX);
+  if (QN) {
+    X[1] = cv.take<T>(batch * sX);
+  } else {
+    X[1] = X[0];
+    XT[0] = cv.take<T>(batch * n * ldm);
+    XT[1] = cv.take<T>(batch * n * ldm);
+  }
   PTO_REQUIRE(!cv.overflow, "newton_schulz_orthogonalize: workspace too small");
   const int nb = (int)batch;
   const int64_t sG = rows * cols;
@@ -149,24 +172,39 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
     return 0;
   }
 
-  // X0 = s·X in both layouts, pads zeroed.
-  if (!transposed) {
-    if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, Xb, ldn, m * ldn, XT[0], ldm, n * ldm, false, nb, stream))
-      return -1;
+  // X0 = s·X (and, without the QN layout, X0ᵀ), pads zeroed.
+  if (QN) {
+    if (!transposed) {
+      if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, X[0], ldn, sX, nullptr, 0, 0, false, nb, stream))
+        return -1;
+    } else {
+      if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, nullptr, 0, 0, X[0], ldn, sX, false, nb, stream))
+        return -1;
+    }
+    // pad columns of the pong buffer, pad rows of both
+    if (launch_zero_cols<T>(X[1], m, ldn, n, sX, nb, stream)) return -1;
+    for (int i = 0; i < 2; ++i)
+      if (launch_zero_cols<T>(X[i] + m * ldn, ldm - m, ldn, 0, sX, nb, stream)) return -1;
   } else {
-    if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, XT[0], ldm, n * ldm, Xb, ldn, m * ldn, false, nb, stream))
-      return -1;
+    if (!transposed) {
+      if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, X[0], ldn, sX, XT[0], ldm, n * ldm, false, nb, stream))
+        return -1;
+    } else {
+      if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, XT[0], ldm, n * ldm, X[0], ldn, sX, false, nb, stream))
+        return -1;
+    }
+    if (launch_zero_cols<T>(XT[1], n, ldm, m, n * ldm, nb, stream)) return -1;
   }
-  if (launch_zero_cols<T>(XT[1], n, ldm, m, n * ldm, nb, stream)) return -1;
   if (launch_zero_cols<T>(Ab, m, ldm, m, m * ldm, nb, stream)) return -1;
   if (launch_zero_cols<T>(Bb, m, ldm, m, m * ldm, nb, stream)) return -1;
 
-  int cur = 0;  // XT[cur] holds X_tᵀ
+  int cur = 0;  // X[cur] (QN) or XT[cur] holds the current iterate
   for (int64_t t = 0; t < steps; ++t) {
     const bool last = t == steps - 1;
+    T* Xc = X[cur];
     // 1. A = X·Xᵀ
     {
-      GemmArgs g{Xb, ldn, m * ldn, Xb, ldn, m * ldn, (int)m, (int)m, (int)ldn, 0, 0, nullptr};
+      GemmArgs g{Xc, ldn, sX, Xc, ldn, sX, (int)m, (int)m, (int)ldn, 0, 0, nullptr};
       EpiStore<T, A> e{Ab, ldm, m * ldm, vec_ok<T>(Ab, ldm, m * ldm)};
       if (launch_gemm<T, true>(g, e, nb, stream, "ns5_gram")) return -1;
     }
@@ -177,12 +215,15 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
                       vec_ok<T>(Ab, ldm, m * ldm) && vec_ok<T>(Bb, ldm, m * ldm)};
       if (launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
     }
-    // 3. X' = B'·X   (as B'·(Xᵀ)ᵀ over the stored transpose)
+    // 3. X' = B'·X   (QN: over X itself; else as B'·(Xᵀ)ᵀ over the stored
+    //    transpose, X written in place since this product does not read it)
     {
-      GemmArgs g{Bb, ldm, m * ldm, XT[cur], ldm, n * ldm, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
       EpiNsUpdate<T, A> e{};
-      if (!last) {
-        e.dst = Xb; e.ld_d = ldn; e.s_d = m * ldn;
+      if (!last && QN) {
+        e.dst = X[cur ^ 1]; e.ld_d = ldn; e.s_d = sX;
+        e.dstT = nullptr;
+      } else if (!last) {
+        e.dst = X[0]; e.ld_d = ldn; e.s_d = sX;
         e.dstT = XT[cur ^ 1]; e.ld_t = ldm; e.s_t = n * ldm;
       } else if (!transposed) {
         e.dst = out; e.ld_d = cols; e.s_d = sG;
@@ -193,7 +234,13 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
       }
       e.vec_d = e.dst && vec_ok<T>(e.dst, e.ld_d, e.s_d);
       e.vec_t = e.dstT && vec_ok<T>(e.dstT, e.ld_t, e.s_t);
-      if (launch_gemm<T, false>(g, e, nb, stream, "ns5_update")) return -1;
+      if constexpr (QN) {
+        GemmArgs g{Bb, ldm, m * ldm, Xc, ldn, sX, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
+        if (launch_gemm_qn(g, e, nb, stream, "ns5_update")) return -1;
+      } else {
+        GemmArgs g{Bb, ldm, m * ldm, XT[cur], ldm, n * ldm, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
+        if (launch_gemm<T, false>(g, e, nb, stream, "ns5_update")) return -1;
+      }
     }
     cur ^= 1;
   }

@@ -44,8 +44,10 @@ def test_version_and_workspace_queries(lib):
     ws_small = L.pto_ns5_workspace_bytes(2, 1, 512, 256)
     ws_big = L.pto_ns5_workspace_bytes(2, 32, 4096, 11008)
     assert 0 < ws_small < ws_big
-    # bf16 NS5 workspace: A, B (m²) + X, 2·Xᵀ (m·n) per matrix
-    assert ws_big >= 32 * 2 * (2 * 4096 * 4096 + 3 * 4096 * 11008)
+    # bf16 NS5 workspace: A, B (m²) + two X buffers (m·n) per matrix
+    assert ws_big >= 32 * 2 * (2 * 4096 * 4096 + 2 * 4096 * 11008)
+    # fp32 keeps X and a pair of stored Xᵀ
+    assert L.pto_ns5_workspace_bytes(0, 32, 4096, 11008) >= 32 * 4 * (2 * 4096 * 4096 + 3 * 4096 * 11008)
     assert L.pto_ns5_workspace_bytes(9, 1, 8, 8) == 0  # unknown dtype
     assert L.pto_kron_workspace_bytes(0, 4096, 4096) >= 4096 * 4096 * 4
     assert L.pto_inverse_root_workspace_bytes(1, 1, 1024, 100) > 10 * 1024 * 1024 * 8

@@ -76,7 +76,10 @@ def test_ns5_empty(native_backend):
         assert got.shape == shape
 
 
-@pytest.mark.parametrize("shape", [(256, 512), (1024, 1024), (2, 384, 1000), (1000, 384)])
+@pytest.mark.parametrize("shape", [(256, 512), (1024, 1024), (2, 384, 1000), (1000, 384),
+                                   # ragged: zero pad rows/columns of X, partial output tiles
+                                   (37, 100), (100, 37), (3, 70, 130), (129, 65), (5, 8), (300, 1030),
+                                   (64, 300, 1030)])  # 640 tiles: the 256 x 256 tile path, ragged
 def test_ns5_bf16_vs_oracle(native_backend, shape):
     G = (torch.randn(*shape) * 1e-3).bfloat16()
     want = oo.ns5(G.float().numpy())  # fp32 work, like the reference's upcast
