@@ -241,7 +241,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   __shared__ __attribute__((aligned(16))) char st3[Plan::ARR];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  // wave index in a scalar register: DMA destinations and per-wave offsets
+  // are then scalar arithmetic
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
   const int ntile = gridDim.x;  // tiles per matrix
   const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y);
@@ -258,34 +260,36 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // QN layout a Q lane supplies row rq = byte offset / QRB, physical chunk
   // L % CPR, logical chunk (L % CPR) ^ swzq(rq); columns past the row
   // pitch re-read its last chunk.
-  const T* src[IPW];
-  int64_t step[IPW];  // elements between consecutive K tiles
+  const char* src[IPW];
+  unsigned step[IPW];  // bytes between consecutive K tiles (the launcher bounds it)
   int dst_off[IPW];
 #pragma unroll
   for (int q = 0; q < IPW; ++q) {
     const int R0 = 16 * (wave * IPW + q), r = R0 + (lane >> 2);
     const int chunk = (lane & 3) ^ swz(r);
+    const T* s;
     if (R0 < BM) {
       const int gr = min(row0 + r, max(g.M - 1, 0));
-      src[q] = static_cast<const T*>(g.P) + (int64_t)b * g.sP + (int64_t)gr * g.ldp + chunk * VEC;
-      step[q] = BK;
+      s = static_cast<const T*>(g.P) + (int64_t)b * g.sP + (int64_t)gr * g.ldp + chunk * VEC;
+      step[q] = kRowBytes;
     } else if (!QN) {
       const int gr = min(col0 + (r - BM), max(g.N - 1, 0));
-      src[q] = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)gr * g.ldq + chunk * VEC;
-      step[q] = BK;
+      s = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)gr * g.ldq + chunk * VEC;
+      step[q] = kRowBytes;
     } else {
       const int rq = (R0 - BM) * kRowBytes / QRB + lane / CPR;
       const int c = (lane % CPR) ^ swzq(rq);
       const int64_t col = min((int64_t)col0 + c * VEC, g.ldq - VEC);
-      src[q] = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)rq * g.ldq + col;
-      step[q] = (int64_t)BK * g.ldq;
+      s = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)rq * g.ldq + col;
+      step[q] = (unsigned)(kRowBytes * g.ldq);
     }
+    src[q] = reinterpret_cast<const char*>(s);
     dst_off[q] = R0 * kRowBytes;
   }
   auto issue = [&](int kt, char* stage) {
 #pragma unroll
     for (int q = 0; q < IPW; ++q)
-      __builtin_amdgcn_global_load_lds((gbl_void_t*)(src[q] + (int64_t)kt * step[q]),
+      __builtin_amdgcn_global_load_lds((gbl_void_t*)(src[q] + (uint64_t)(unsigned)kt * step[q]),
                                        (lds_void_t*)(stage + dst_off[q]), 16, 0, 0);
   };
 
@@ -311,15 +315,20 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       qoff[fn] = qr * QRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
     }
   }
-  auto compute = [&](const char* stage) {
+  // One K tile's MFMA operands for this wave.
+  struct Frag {
+    uint4 a[NRG][FM], b[NRG][FN];
+  };
+  constexpr int kTileMfma = NRG * IPR * FM * FN;  // MFMAs per K tile
+  static_assert(kTileMfma % IPW == 0, "MFMA groups between DMA instructions");
+  auto load_frags = [&](const char* stage, Frag& f) {
     const char* Pw = stage + (wm * WTM + lr) * kRowBytes;
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       const int off = ((lg * NRG + rg) ^ sw) * 16;
-      uint4 a[FM], bq[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
-        a[fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
+        f.a[rg][fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
       if constexpr (QN) {
         // lanes of k-half lg, step rg: k = 16*lg + 8*rg + 0..7
         const char* Qs = stage + BM * kRowBytes + 8 * rg * QRB;
@@ -328,38 +337,75 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
           v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(Qs + qoff[fn]));
           v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(Qs + qoff[fn] + 4 * QRB));
           uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
-          bq[fn] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+          f.b[rg][fn] = make_uint4(l2.x, l2.y, h2.x, h2.y);
         }
       } else {
         const char* Qw = stage + (BM + wn * WTN + lr) * kRowBytes;
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn)
-          bq[fn] = *reinterpret_cast<const uint4*>(Qw + fn * MF::MN * kRowBytes + off);
+          f.b[rg][fn] = *reinterpret_cast<const uint4*>(Qw + fn * MF::MN * kRowBytes + off);
       }
+    }
+  };
+  auto zero_frags = [&](Frag& f) {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) f.a[rg][fm] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) f.b[rg][fn] = make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto mma = [&](const Frag& f) {
+#pragma unroll
+    for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
       for (int ii = 0; ii < IPR; ++ii)
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MF::mma(a[fm], bq[fn], ii, acc[fm][fn]);
-    }
+          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MF::mma(f.a[rg][fm], f.b[rg][fn], ii, acc[fm][fn]);
   };
 
+  // Skewed pipeline: during step s the wave issues the LDS reads of tile
+  // s+1 into one register set, then the MFMAs of tile s from the other set
+  // (read during step s-1), with the DMA of tile s+3 spread between them;
+  // LDS latency hides behind a whole tile of MFMAs and the memory unit's
+  // queue never holds up MFMA issue. One barrier per step covers both
+  // hazards: every wave has waited for its reads (lgkmcnt(0)) before
+  // arriving, so the stage of tile s-1 may be refilled, and every wave's
+  // part of tile s+1 has landed (vmcnt: only tile s+2 may be outstanding).
+  // Steps past the last K tile (the unrolled group's tail) multiply zeroed
+  // operands, so the MFMAs need no branch.
   const int KT = g.K / BK;
   if (KT > 0) {
+    Frag f0, f1;
     issue(0, st0);
     issue(min(1, KT - 1), st1);
     issue(min(2, KT - 1), st2);
+    __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));
+    stage_barrier();
+    load_frags(st0, f0);
     for (int kt = 0; kt < KT; kt += kStages) {
-#define PTO_STEP(J, CUR, NXT)                                 \
-  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));             \
-  stage_barrier();                                            \
-  issue(min(kt + (J) + 3, KT - 1), NXT);                      \
-  if (kt + (J) < KT) compute(CUR);
-      PTO_STEP(0, st0, st3)
-      PTO_STEP(1, st1, st0)
-      PTO_STEP(2, st2, st1)
-      PTO_STEP(3, st3, st2)
+      // J: step in the unrolled group; RD: stage of tile kt+J+1; DMA:
+      // stage of tile kt+J+3
+#define PTO_STEP(J, CUR, NXT, RD, DMA)                             \
+  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(IPW));                      \
+  stage_barrier();                                                 \
+  if (kt + (J) + 1 < KT)                                           \
+    load_frags(RD, NXT);                                           \
+  else                                                             \
+    zero_frags(NXT);                                               \
+  issue(min(kt + (J) + 3, KT - 1), DMA);                           \
+  mma(CUR);                                                        \
+  for (int q = 0; q < IPW; ++q) {                                  \
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);             \
+    __builtin_amdgcn_sched_group_barrier(0x008, kTileMfma / IPW, 0); \
+  }
+      PTO_STEP(0, f0, f1, st1, st3)
+      PTO_STEP(1, f1, f0, st2, st0)
+      PTO_STEP(2, f0, f1, st3, st1)
+      PTO_STEP(3, f1, f0, st0, st2)
 #undef PTO_STEP
     }
     __builtin_amdgcn_s_waitcnt(PTO_VMCNT(0));  // stray prefetches land before reuse
@@ -567,6 +613,7 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
   typedef typename TileSet<bf16>::small Small;
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
   PTO_REQUIRE(g.K % Big::BK == 0 && g.K % Small::BK == 0, std::string(name) + ": K not padded");
+  PTO_REQUIRE(g.ldq < (int64_t(1) << 26), std::string(name) + ": row pitch too large");  // 64-byte K steps in 32 bits
   PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
