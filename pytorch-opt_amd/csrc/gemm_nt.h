@@ -6,8 +6,8 @@
 // fragment a contiguous 16-byte run in LDS for all three element types.
 //
 // Operand contract (checked by the host launchers):
-//   * K is a multiple of the tile's BK and the pad columns of both operands
-//     are zero (workspace buffers are padded to kPadK elements);
+//   * K is a multiple of four K tiles (kStages * BK) and the pad columns of
+//     both operands are zero (workspace buffers are padded to kPadK);
 //   * rows beyond M (P) or N (Q) are never read (masked to zero);
 //   * operand base pointers and leading dimensions are 16-byte aligned.
 //
@@ -319,8 +319,13 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   struct Frag {
     uint4 a[NRG][FM], b[NRG][FN];
   };
-  constexpr int kTileMfma = NRG * IPR * FM * FN;  // MFMAs per K tile
-  static_assert(kTileMfma % IPW == 0, "MFMA groups between DMA instructions");
+  constexpr int kTileMfma = NRG * IPR * FM * FN;              // MFMAs per K tile
+  constexpr int kFragReads = NRG * (FM + (QN ? 2 : 1) * FN);  // LDS reads per K tile
+  static_assert(kTileMfma % IPW == 0 && kFragReads % IPW == 0, "schedule groups");
+  // Order within a step: LDS reads for the next tile all first, or spread
+  // between the MFMA groups (measured faster for the QN layout, slower for
+  // the symmetric K-contiguous products).
+  constexpr bool kSpreadReads = QN;
   auto load_frags = [&](const char* stage, Frag& f) {
     const char* Pw = stage + (wm * WTM + lr) * kRowBytes;
 #pragma unroll
@@ -347,15 +352,6 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       }
     }
   };
-  auto zero_frags = [&](Frag& f) {
-#pragma unroll
-    for (int rg = 0; rg < NRG; ++rg) {
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm) f.a[rg][fm] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int fn = 0; fn < FN; ++fn) f.b[rg][fn] = make_uint4(0, 0, 0, 0);
-    }
-  };
   auto mma = [&](const Frag& f) {
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg)
@@ -375,8 +371,8 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // hazards: every wave has waited for its reads (lgkmcnt(0)) before
   // arriving, so the stage of tile s-1 may be refilled, and every wave's
   // part of tile s+1 has landed (vmcnt: only tile s+2 may be outstanding).
-  // Steps past the last K tile (the unrolled group's tail) multiply zeroed
-  // operands, so the MFMAs need no branch.
+  // The launchers require K to be a multiple of four tiles, so every step
+  // of the unrolled group is a real one and the MFMAs need no branch.
   const int KT = g.K / BK;
   if (KT > 0) {
     Frag f0, f1;
@@ -389,18 +385,19 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     for (int kt = 0; kt < KT; kt += kStages) {
       // J: step in the unrolled group; RD: stage of tile kt+J+1; DMA:
       // stage of tile kt+J+3
-#define PTO_STEP(J, CUR, NXT, RD, DMA)                             \
-  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(IPW));                      \
-  stage_barrier();                                                 \
-  if (kt + (J) + 1 < KT)                                           \
-    load_frags(RD, NXT);                                           \
-  else                                                             \
-    zero_frags(NXT);                                               \
-  issue(min(kt + (J) + 3, KT - 1), DMA);                           \
-  mma(CUR);                                                        \
-  for (int q = 0; q < IPW; ++q) {                                  \
-    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);             \
-    __builtin_amdgcn_sched_group_barrier(0x008, kTileMfma / IPW, 0); \
+#define PTO_STEP(J, CUR, NXT, RD, DMA)                                \
+  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(IPW));                         \
+  stage_barrier();                                                    \
+  load_frags(RD, NXT);                                                \
+  issue(min(kt + (J) + 3, KT - 1), DMA);                              \
+  mma(CUR);                                                           \
+  if constexpr (!kSpreadReads)                                        \
+    __builtin_amdgcn_sched_group_barrier(0x100, kFragReads, 0);       \
+  for (int q = 0; q < IPW; ++q) {                                     \
+    if constexpr (kSpreadReads)                                       \
+      __builtin_amdgcn_sched_group_barrier(0x100, kFragReads / IPW, 0); \
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                \
+    __builtin_amdgcn_sched_group_barrier(0x008, kTileMfma / IPW, 0);  \
   }
       PTO_STEP(0, f0, f1, st1, st3)
       PTO_STEP(1, f1, f0, st2, st0)
@@ -592,7 +589,7 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
   static_assert(!UPPER || (Big::BM == Big::BN && Small::BM == Small::BN), "symmetric products need square tiles");
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
   PTO_REQUIRE(!UPPER || g.M == g.N, std::string(name) + ": symmetric product needs M == N");
-  PTO_REQUIRE(g.K % Small::BK == 0 && g.K % Big::BK == 0, std::string(name) + ": K not padded");
+  PTO_REQUIRE(g.K % (kStages * Small::BK) == 0 && g.K % (kStages * Big::BK) == 0, std::string(name) + ": K not padded");
   PTO_REQUIRE(g.ldp % (16 / sizeof(T)) == 0 && g.ldq % (16 / sizeof(T)) == 0 &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
@@ -612,7 +609,7 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
   typedef typename TileSet<bf16>::big Big;
   typedef typename TileSet<bf16>::small Small;
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
-  PTO_REQUIRE(g.K % Big::BK == 0 && g.K % Small::BK == 0, std::string(name) + ": K not padded");
+  PTO_REQUIRE(g.K % (kStages * Big::BK) == 0 && g.K % (kStages * Small::BK) == 0, std::string(name) + ": K not padded");
   PTO_REQUIRE(g.ldq < (int64_t(1) << 26), std::string(name) + ": row pitch too large");  // 64-byte K steps in 32 bits
   PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,

@@ -18,8 +18,9 @@ enum Dtype : int { kF32 = 0, kF64 = 1, kBF16 = 2 };
 typedef __bf16 bf16;
 
 // Every operand buffer the kernels read along K has its leading dimension
-// padded to a multiple of this many elements, with the pad columns zeroed.
-constexpr int kPadK = 64;
+// padded to a multiple of this many elements, with the pad columns zeroed:
+// four 64-byte K tiles of bf16 (eight of fp32), the MFMA core's unroll.
+constexpr int kPadK = 128;
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
