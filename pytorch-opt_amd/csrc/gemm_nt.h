@@ -25,6 +25,7 @@
 namespace pto {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef double f64x4_t __attribute__((ext_vector_type(4)));
 
@@ -35,17 +36,22 @@ typedef double f64x4_t __attribute__((ext_vector_type(4)));
 template <typename T>
 struct Mfma;
 
+// bf16 uses the 16x16x32 shape: for the same wave tile it gives four times
+// as many independent accumulators as 32x32x16 at the same operand reads
+// and registers, and measured faster in this core. Lane l feeds row (or
+// column) l % 16 with k = 8*(l/16) .. +7 (both operands use the same k
+// assignment, so the sum is exact whatever order the hardware uses).
 template <>
-struct Mfma<bf16> {  // v_mfma_f32_32x32x16_bf16
+struct Mfma<bf16> {  // v_mfma_f32_16x16x32_bf16
   typedef float acc_t;
-  typedef f32x16_t cvec_t;
-  static constexpr int MN = 32, KPL = 8, G = 2, NACC = 16;
+  typedef f32x4_t cvec_t;
+  static constexpr int MN = 16, KPL = 8, G = 4, NACC = 4;
   __device__ static __forceinline__ cvec_t mma(const uint4& a, const uint4& b, int, cvec_t c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
-  __device__ static __forceinline__ int row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
-  __device__ static __forceinline__ int col(int lane, int) { return lane & 31; }
+  __device__ static __forceinline__ int row(int lane, int r) { return (lane >> 4) * 4 + r; }
+  __device__ static __forceinline__ int col(int lane, int) { return lane & 15; }
 };
 
 template <>
@@ -158,9 +164,12 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 2) & 3) ^ (r & 2); }
 // MFMA B fragments come from transposing LDS reads (ds_read_b64_tr_b16).
 // Within each 16-lane group, lane s addresses 4 elements at row k0 + s/4,
 // column n0 + 4*(s%4); lane s then receives column n0 + s of rows
-// k0..k0+3. 16-byte chunk c of Q row r lives at physical chunk
-// c ^ (4 * (r % 4)): the four rows of one read land in distinct banks.
-__device__ __forceinline__ int swzq(int r) { return 4 * (r & 3); }
+// k0..k0+3. With the 16x16x32 MFMA, 16-lane group g holds k = 8g..8g+7,
+// so one read covers rows {4t..4t+3} + 8g and two 16-byte chunks per
+// group. Q rows are 256 or 512 bytes, so a row's banks depend only on the
+// chunk: 16-byte chunk c of Q row r lives at physical chunk c ^ swzq(r),
+// which is distinct (mod 16) across the 8 rows a half-wave reads.
+__device__ __forceinline__ int swzq(int r) { return 2 * ((r & 3) | ((r >> 1) & 4)); }
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
@@ -304,14 +313,16 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const int lr = lane % MF::MN, lg = lane / MF::MN;
   const int sw = swz(lr);  // rows of every fragment are lr mod 16
   // QN: byte offset of this lane's transposing read for fragment fn, MFMA
-  // step 0, first half; step rg and the second half (k + 4) add whole rows,
-  // which keep the row's swizzle (row % 4 = (lane % 16) / 4).
+  // step 0, first half (k = KSPAN*lg + 0..3); step rg (8 rows) and the
+  // second half (4 rows) add rows that keep the row's swizzle, which
+  // depends on row bits 0, 1 and 3 only.
   int qoff[FN];
   if constexpr (QN) {
-    const int li = lane & 15, qr = 16 * lg + (li >> 2);
+    static_assert(KSPAN % 8 == 0, "QN row steps must keep the swizzle");
+    const int li = lane & 15, qr = KSPAN * lg + (li >> 2);
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
-      const int col = wn * WTN + fn * MF::MN + 16 * ((lane >> 4) & 1) + 4 * (li & 3);
+      const int col = wn * WTN + fn * MF::MN + (lane & (MF::MN - 1) & ~15) + 4 * (li & 3);
       qoff[fn] = qr * QRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
     }
   }
@@ -335,7 +346,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       for (int fm = 0; fm < FM; ++fm)
         f.a[rg][fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
       if constexpr (QN) {
-        // lanes of k-half lg, step rg: k = 16*lg + 8*rg + 0..7
+        // lanes of k-group lg, step rg: k = KSPAN*lg + 8*rg + 0..7
         const char* Qs = stage + BM * kRowBytes + 8 * rg * QRB;
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
