@@ -10,20 +10,35 @@
 
 namespace pto {
 
-constexpr int kRedBlocks = 64;  // partial sums per matrix
+constexpr int kRedBlocks = 256;  // partial sums per matrix
 
-// partial[b][blk] = sum of x^2 over a strided slice of matrix b (double).
+// partial[b][blk] = sum of x^2 over rows blk, blk + kRedBlocks, ... of
+// matrix b (double accumulation, fixed order, so deterministic). Rows are
+// read as 16-byte runs when the pitch and base allow.
 template <typename T>
 __global__ void __launch_bounds__(256) sumsq_partial_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
                                                             int64_t ld, int64_t sb, double* __restrict__ partial) {
+  constexpr int VEC = 16 / (int)sizeof(T);
   const int b = blockIdx.y;
   const T* xb = x + (int64_t)b * sb;
-  const int64_t total = rows * cols;
+  const bool vec = ld % VEC == 0 && (reinterpret_cast<uintptr_t>(xb) & 15) == 0;
+  const int64_t nv = vec ? cols / VEC : 0;  // whole 16-byte runs per row
   double s = 0.0;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    int64_t r = e / cols, c = e - r * cols;
-    double v = to_f(xb[r * ld + c]);
-    s += v * v;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const T* row = xb + r * ld;
+    for (int64_t v = threadIdx.x; v < nv; v += blockDim.x) {
+      const uint4 u = reinterpret_cast<const uint4*>(row)[v];
+      const T* e = reinterpret_cast<const T*>(&u);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const double d = to_f(e[k]);
+        s += d * d;
+      }
+    }
+    for (int64_t c = nv * VEC + threadIdx.x; c < cols; c += blockDim.x) {
+      const double d = to_f(row[c]);
+      s += d * d;
+    }
   }
   __shared__ double red[256];
   red[threadIdx.x] = s;
@@ -124,12 +139,66 @@ __global__ void __launch_bounds__(256) pack_kernel_f64(const TI* __restrict__ in
   }
 }
 
+// Straight copy only (no transposed output, no ones column): rows of 16-byte
+// runs, out(r, c) = s_b * in(r, c) for c < cols and 0 for cols <= c < ld_out.
+// Same value conversion as pack_kernel. Needs 16-byte aligned bases and
+// pitches that are multiples of 16 bytes; TI and TO of the same 2- or
+// 4-byte size.
+template <typename TI, typename TO, typename S>
+__global__ void __launch_bounds__(256) pack_rows_kernel(const TI* __restrict__ in, int64_t rows, int64_t cols,
+                                                        int64_t ld_in, int64_t s_in, const S* __restrict__ scale,
+                                                        TO* __restrict__ out, int64_t ld_out, int64_t s_out) {
+  static_assert(sizeof(TI) == sizeof(TO) && sizeof(TI) <= 4, "same 2- or 4-byte types");
+  constexpr int VEC = 16 / (int)sizeof(TI);
+  const int b = blockIdx.y;
+  const TI* ib = in + (int64_t)b * s_in;
+  TO* ob = out + (int64_t)b * s_out;
+  const S sc = scale ? scale[b] : S(1);
+  const int64_t nchunk = ld_out / VEC;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const TI* irow = ib + r * ld_in;
+    TO* orow = ob + r * ld_out;
+    for (int64_t ch = threadIdx.x; ch < nchunk; ch += blockDim.x) {
+      const int64_t c0 = ch * VEC;
+      uint4 uo;
+      TO* o = reinterpret_cast<TO*>(&uo);
+      if (c0 + VEC <= cols) {
+        const uint4 ui = reinterpret_cast<const uint4*>(irow)[ch];
+        const TI* e = reinterpret_cast<const TI*>(&ui);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) o[k] = static_cast<TO>(static_cast<float>(static_cast<S>(to_f(e[k])) * sc));
+      } else {
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          const int64_t c = c0 + k;
+          o[k] = static_cast<TO>(c < cols ? static_cast<float>(static_cast<S>(to_f(irow[c])) * sc) : 0.f);
+        }
+      }
+      reinterpret_cast<uint4*>(orow)[ch] = uo;
+    }
+  }
+}
+
 // Host wrapper. The grid covers the padded extents of both outputs.
 template <typename TI, typename TO, typename S>
 int launch_pack(const TI* in, int64_t rows, int64_t cols, int64_t ld_in, int64_t s_in, const S* scale, TO* out_s,
                 int64_t ld_s, int64_t s_s, TO* out_t, int64_t ld_t, int64_t s_t, bool ones, int batch,
                 hipStream_t stream) {
   if (batch == 0) return 0;
+  if constexpr (sizeof(TI) == sizeof(TO) && sizeof(TI) <= 4 && sizeof(S) == 4) {
+    constexpr int VEC = 16 / (int)sizeof(TI);
+    const bool rows_ok = out_t == nullptr && !ones && out_s != nullptr && ld_in % VEC == 0 && ld_s % VEC == 0 &&
+                         s_in % VEC == 0 && s_s % VEC == 0 && (reinterpret_cast<uintptr_t>(in) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(out_s) & 15) == 0;
+    if (rows_ok) {
+      PTO_REQUIRE(batch < 65536, "pack: grid too large");
+      const unsigned gx = (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, 1024));
+      hipLaunchKernelGGL((pack_rows_kernel<TI, TO, S>), dim3(gx, (unsigned)batch), dim3(256), 0, stream, in, rows,
+                         cols, ld_in, s_in, scale, out_s, ld_s, s_s);
+      PTO_LAUNCHED("pack_rows");
+      return 0;
+    }
+  }
   int64_t rext = rows, cext = cols + (ones ? 1 : 0);
   if (out_s) cext = std::max<int64_t>(cext, ld_s);
   if (out_t) rext = std::max<int64_t>(rext, ld_t);
