@@ -498,14 +498,16 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
       epi.put(b, i, j0, v, kbeg, n, pre[it], vo);
-      if (need_t) {
+      if (need_t && !Epi::kVoIsV) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];
       }
     }
     if (need_t) {
-      __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-      __builtin_amdgcn_wave_barrier();
+      if constexpr (!Epi::kVoIsV) {  // the write-back above must land first
+        __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+        __builtin_amdgcn_wave_barrier();
+      }
       // output row j = wc0 + c, columns i = pr0 + r..r+7
       typename Epi::PreT pret[ITEMS_T];
 #pragma unroll
@@ -642,6 +644,8 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
 //       (the mirror of a symmetric product, or a transposed copy);
 //   has_t()                              whether put_t is needed outside
 //       symmetric products;
+//   kVoIsV                               vo is always v (the staged values
+//       then serve the transposed pass as they are);
 //   finish(b)                            once per thread at the end.
 // j0 and i0 are multiples of 8; `vec` (set by the host when the row pitch,
 // batch stride and base allow) enables 16-byte accesses for full runs.
@@ -772,6 +776,7 @@ struct EpiStore {
   bool vec;
   typedef NoPre Pre;
   typedef NoPre PreT;
+  static constexpr bool kVoIsV = true;
   __device__ __forceinline__ bool has_t() const { return false; }
   __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
   __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
@@ -796,6 +801,7 @@ struct EpiBlend {
   bool vec;
   typedef Raw8<TO> Pre;
   typedef Raw8<TO> PreT;
+  static constexpr bool kVoIsV = true;
   __device__ __forceinline__ bool has_t() const { return false; }
   __device__ __forceinline__ void load(int b, int i, int j0, int kbeg, int n, Pre& p) const {
     if (beta != A(0)) ld8_pre<TO>(dst + (int64_t)b * sd + (int64_t)i * ld + j0, p, kbeg, n, vec);

@@ -49,6 +49,7 @@ struct EpiNsSq {
   bool vec;
   typedef Raw8<T> Pre;
   typedef NoPre PreT;
+  static constexpr bool kVoIsV = false;  // the mirror stores B', not the raw product
   __device__ __forceinline__ bool has_t() const { return false; }
   __device__ __forceinline__ void load(int b, int i, int j0, int kbeg, int n, Pre& p) const {
     ld8_pre<T>(Asrc + (int64_t)b * sd + (int64_t)i * ld + j0, p, kbeg, n, vec);
@@ -80,6 +81,7 @@ struct EpiNsUpdate {
   bool vec_d, vec_t;
   typedef NoPre Pre;
   typedef NoPre PreT;
+  static constexpr bool kVoIsV = true;
   __device__ __forceinline__ bool has_t() const { return dstT != nullptr; }
   __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
   __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}

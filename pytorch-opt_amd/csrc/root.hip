@@ -142,6 +142,7 @@ struct EpiMk {
   bool vec;
   typedef NoPre Pre;
   typedef NoPre PreT;
+  static constexpr bool kVoIsV = true;
   __device__ __forceinline__ bool has_t() const { return false; }
   __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
   __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
