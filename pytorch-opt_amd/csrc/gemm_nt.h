@@ -20,6 +20,8 @@
 // three K tiles ahead of the MFMAs; one barrier per K tile (details below).
 #pragma once
 
+#include <atomic>
+
 #include "pto_common.h"
 
 namespace pto {
@@ -542,9 +544,11 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 // ------------------------------------------------------------- host launch
 
 // Tile choices per element type: full products and symmetric (upper-tile)
-// products, each with a "big" tile for large problems and a "small" one
-// when the big tiles would leave most of the 256 CUs idle. Symmetric
-// products need square tiles.
+// products, each with a "big" tile and a "small" one. Symmetric products
+// need square tiles. kBigRate is the big tile's throughput per CU relative
+// to the small tile's (area per unit time, measured on MI355X over square
+// and rectangular products from 512 to 11008): the big tile reuses each
+// staged operand byte for more MFMA work.
 template <typename T>
 struct TileSet;
 template <>
@@ -553,6 +557,7 @@ struct TileSet<bf16> {
   typedef Tile<128, 128, 32, 2, 2> small;
   typedef Tile<256, 256, 32, 2, 4> sym_big;
   typedef Tile<128, 128, 32, 2, 2> sym_small;
+  static constexpr double kBigRate = 1.5;
 };
 template <>
 struct TileSet<float> {
@@ -560,6 +565,7 @@ struct TileSet<float> {
   typedef Tile<64, 64, 16, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
+  static constexpr double kBigRate = 1.22;
 };
 template <>
 struct TileSet<double> {
@@ -567,7 +573,35 @@ struct TileSet<double> {
   typedef Tile<32, 32, 8, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
+  static constexpr double kBigRate = 1.25;
 };
+
+// Compute units of the current device (256 on a full MI355X), cached per
+// device ordinal.
+inline int device_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Tiles are spread over the CUs, so the product ends when the busiest CU has
+// run ceil(tiles / CUs) of them. Pick the tile size whose busiest CU covers
+// the least area after weighting by the big tile's higher rate. At the same
+// number of tiles per CU the big tile wins; a big tiling that leaves half
+// the CUs idle (e.g. 64 big tiles against 256 small ones) loses.
+template <typename T, class Big, class Small>
+bool prefer_big_tiles(int64_t big_tiles, int64_t small_tiles) {
+  const int64_t cus = device_cus();
+  const double big_load = double((big_tiles + cus - 1) / cus) * (Big::BM * Big::BN);
+  const double small_load = double((small_tiles + cus - 1) / cus) * (Small::BM * Small::BN);
+  return big_load < small_load * TileSet<T>::kBigRate;
+}
 
 template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false>
 int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
@@ -607,9 +641,12 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
-  int64_t tm = (g.M + Big::BM - 1) / Big::BM, tn = (g.N + Big::BN - 1) / Big::BN;
-  int64_t big_tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
-  if (big_tiles >= 512) return launch_gemm_cfg<T, Big, UPPER, Epi>(g, epi, batch, stream, name);
+  const int64_t tm = (g.M + Big::BM - 1) / Big::BM, tn = (g.N + Big::BN - 1) / Big::BN;
+  const int64_t sm = (g.M + Small::BM - 1) / Small::BM, sn = (g.N + Small::BN - 1) / Small::BN;
+  const int64_t big_tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
+  const int64_t small_tiles = (UPPER ? sm * (sm + 1) / 2 : sm * sn) * batch;
+  if (prefer_big_tiles<T, Big, Small>(big_tiles, small_tiles))
+    return launch_gemm_cfg<T, Big, UPPER, Epi>(g, epi, batch, stream, name);
   return launch_gemm_cfg<T, Small, UPPER, Epi>(g, epi, batch, stream, name);
 }
 
@@ -627,8 +664,10 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
   PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
-  int64_t big_tiles = (int64_t)((g.M + Big::BM - 1) / Big::BM) * ((g.N + Big::BN - 1) / Big::BN) * batch;
-  if (big_tiles >= 512) return launch_gemm_cfg<bf16, Big, false, Epi, true>(g, epi, batch, stream, name);
+  const int64_t big_tiles = (int64_t)((g.M + Big::BM - 1) / Big::BM) * ((g.N + Big::BN - 1) / Big::BN) * batch;
+  const int64_t small_tiles = (int64_t)((g.M + Small::BM - 1) / Small::BM) * ((g.N + Small::BN - 1) / Small::BN) * batch;
+  if (prefer_big_tiles<bf16, Big, Small>(big_tiles, small_tiles))
+    return launch_gemm_cfg<bf16, Big, false, Epi, true>(g, epi, batch, stream, name);
   return launch_gemm_cfg<bf16, Small, false, Epi, true>(g, epi, batch, stream, name);
 }
 
