@@ -6,6 +6,16 @@ spectral / RMS-matching learning-rate scale (:52-58) and the step (:60-102):
 per routed parameter buf = μ·buf + g, u = g + μ·buf (Nesterov) or buf,
 O = NS5(u reshaped to (rows, -1)), p ← p·(1 − lr·wd) − lr·scale·O;
 everything else takes the shared AdamW fallback.
+
+Unlike the reference, which orthogonalises one parameter per call, the
+routed parameters of a group are bucketed by (2-D shape, dtype, device)
+and each bucket is orthogonalised by one batched NS5 launch (up to
+``ns_batch_bytes`` of stacked input per launch). NS5 treats every matrix
+of a batch independently, so the parameters end where the per-parameter
+loop would put them; the batched launch fills the GPU where one 2048²
+matrix cannot. The ``update_rms`` diagnostic is summed in the reference's
+parameter order from per-parameter sums read back with one host
+synchronisation per step instead of one per parameter.
 """
 
 from __future__ import annotations
@@ -59,6 +69,34 @@ class Muon(Optimizer, DiagnosticsMixin):
             return 0.2 * max(rows, cols) ** 0.5
         return 1.0
 
+    # Stacked NS5 input per batched launch, in bytes; 0 orthogonalises each
+    # parameter on its own, as the reference does.
+    ns_batch_bytes = 4 << 30
+
+    def _orthogonalize_bucket(self, group, items, contrib):
+        """NS5 of the bucket's stacked matrices, then each parameter's update."""
+        limit = self.ns_batch_bytes
+        start = 0
+        while start < len(items):
+            end = start + 1
+            per = items[start][1].numel() * items[start][1].element_size()
+            while end < len(items) and (end - start + 1) * per <= limit:
+                end += 1
+            chunk = items[start:end]
+            if len(chunk) == 1:
+                outs = [ops.newton_schulz_orthogonalize(chunk[0][1], steps=group["ns_steps"])]
+            else:
+                O = ops.newton_schulz_orthogonalize(torch.stack([u2 for _, u2, _ in chunk]), steps=group["ns_steps"])
+                outs = O.unbind(0)
+            for (p, _, slot), O in zip(chunk, outs):
+                lr_eff = group["lr"] * self._scale(O.shape, group["lr_adjust"])
+                if group["weight_decay"]:
+                    p.mul_(1.0 - group["lr"] * group["weight_decay"])
+                upd = O.reshape(p.shape)
+                p.add_(upd, alpha=-lr_eff)
+                contrib[slot] = (upd.pow(2).sum(), lr_eff, upd.numel())
+            start = end
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
@@ -66,10 +104,10 @@ class Muon(Optimizer, DiagnosticsMixin):
             with torch.enable_grad():
                 loss = closure()
         n_muon = n_adamw = 0
-        sq_sum = 0.0
-        count = 0
+        contrib = []  # per parameter, in order: (sum of upd², lr_eff, numel)
         with StepTimer() as timer:
             for group in self.param_groups:
+                buckets = {}
                 for p in group["params"]:
                     g = p.grad
                     if g is None:
@@ -84,17 +122,28 @@ class Muon(Optimizer, DiagnosticsMixin):
                         buf.mul_(mu).add_(g)
                         u = g.add(buf, alpha=mu) if group["nesterov"] else buf
                         u2 = u if u.ndim == 2 else u.reshape(u.shape[0], -1)
-                        O = ops.newton_schulz_orthogonalize(u2, steps=group["ns_steps"])
-                        lr_eff = group["lr"] * self._scale(O.shape, group["lr_adjust"])
-                        if group["weight_decay"]:
-                            p.mul_(1.0 - group["lr"] * group["weight_decay"])
-                        upd = O.reshape(p.shape)
-                        p.add_(upd, alpha=-lr_eff)
+                        key = (tuple(u2.shape), u2.dtype, u2.device)
+                        buckets.setdefault(key, []).append((p, u2, len(contrib)))
+                        contrib.append(None)
                     else:
                         n_adamw += 1
                         upd, lr_eff = adamw_update(p, g, st, group)
-                    sq_sum += float(upd.pow(2).sum()) * lr_eff * lr_eff
-                    count += upd.numel()
+                        contrib.append((upd.pow(2).sum(), lr_eff, upd.numel()))
+                for items in buckets.values():
+                    self._orthogonalize_bucket(group, items, contrib)
+            sq_sum, count = 0.0, 0
+            if contrib:
+                by_kind = {}
+                for i, (s, _, _) in enumerate(contrib):
+                    by_kind.setdefault((s.device, s.dtype), []).append(i)
+                host = [0.0] * len(contrib)
+                for idx in by_kind.values():
+                    vals = torch.stack([contrib[i][0] for i in idx]).cpu().tolist()
+                    for i, v in zip(idx, vals):
+                        host[i] = v
+                for v, (_, lr_eff, n) in zip(host, contrib):
+                    sq_sum += v * lr_eff * lr_eff
+                    count += n
         self._diag = {"update_rms": (sq_sum / max(count, 1)) ** 0.5, "n_muon_params": n_muon,
                       "n_adamw_params": n_adamw, "step_ms": timer.ms}
         return loss
