@@ -16,8 +16,9 @@ same workload, and secondary figures:
   roots         inverse 4th roots (coupled Newton, fp32) of SPD n = 1024 /
                 2048 / 4096 with λ log-uniform in [1e-6, 1], ε = 1e-6;
   optimizer     Muon + Shampoo steps on the synthetic 12-layer d=2048
-                parameter set (40 steps each), with the CPU oracle's
-                per-step estimate from a bounded sample.
+                parameter set (40 steps each), SOAP on its 48 attention
+                matrices (one refresh period, 10 steps), with the CPU
+                oracle's per-step estimate from a bounded sample.
 """
 
 from __future__ import annotations
@@ -47,6 +48,12 @@ def ns5_kernel_flops(kind, m, n):
     """Algorithmic flops of one NS5 iteration's launch of `kind`, per matrix."""
     m, n = min(m, n), max(m, n)
     return {"ns5_gram": m * (m + 1) * n, "ns5_square": m * m * (m + 1), "ns5_update": 2 * m * m * n}[kind]
+
+
+def soap_matrix_flops(m, n):
+    """Algorithmic flops of one SOAP step (no refresh) of an m x n matrix: the
+    factor update (two symmetric products) and three two-sided rotations."""
+    return m * (m + 1) * n + n * (n + 1) * m + 3 * (2 * m * m * n + 2 * m * n * n)
 
 
 def blas_threads():
@@ -220,17 +227,17 @@ def set_grads(torch, P, step, dev):
 
 
 def bench_optimizer(torch, ops, hip, dev, steps, cpu):
-    from pytorch_opt import Muon, Shampoo
+    from pytorch_opt import SOAP, Muon, Shampoo
 
     mats, vecs = config5_shapes()
     kind = {n: k for n, _, k in mats}
     out = {}
 
-    def run(make_opt):
+    def run(make_opt, n_steps=steps):
         P = config5_params(torch, dev)
         opt = make_opt(P)
         total, per = 0.0, []
-        for t in range(steps):
+        for t in range(n_steps):
             set_grads(torch, P, t, dev)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
@@ -241,7 +248,7 @@ def bench_optimizer(torch, ops, hip, dev, steps, cpu):
             total += dt
         del P, opt
         torch.cuda.empty_cache()
-        return total / steps, per
+        return total / n_steps, per
 
     def make_muon(P):
         routed = [P[n] for n, _, _ in mats]
@@ -254,8 +261,21 @@ def bench_optimizer(torch, ops, hip, dev, steps, cpu):
         return Shampoo([{"params": attn}, {"params": rest, "use_preconditioner": False, "lr": 3e-4}],
                        max_preconditioner_dim=4096, precondition_frequency=20, graft="adagrad")
 
+    def make_soap(P):
+        attn = [P[n] for n, _, _ in mats if kind[n] == "attn"]
+        rest = [P[n] for n, _, _ in mats if kind[n] == "mlp"] + [P[n] for n, _ in vecs] + [P["emb"]]
+        return SOAP([{"params": attn}, {"params": rest, "use_preconditioner": False}], lr=3e-3,
+                    max_preconditioner_dim=4096, precondition_frequency=10)
+
     m_mean, _ = run(make_muon)
     s_mean, s_per = run(make_shampoo)
+    # SOAP: one refresh (step 0, 96 fp64 eigh on torch) and 9 plain steps,
+    # i.e. one precondition_frequency period
+    _, soap_per = run(make_soap, 10)
+    out["soap_refresh_step_ms"] = round(soap_per[0] * 1e3, 1)
+    out["soap_plain_step_ms"] = round(1e3 * sum(soap_per[1:]) / 9, 2)
+    out["soap_step_ms"] = round(1e3 * sum(soap_per) / 10, 2)
+    out["soap_plain_alg_tflops"] = round(48 * soap_matrix_flops(2048, 2048) / (sum(soap_per[1:]) / 9) / 1e12, 2)
     refresh = [s_per[i] for i in range(steps) if i % 20 == 0]
     plain = [s_per[i] for i in range(steps) if i % 20 != 0]
     out["muon_step_ms"] = round(m_mean * 1e3, 2)
@@ -268,6 +288,7 @@ def bench_optimizer(torch, ops, hip, dev, steps, cpu):
     if cpu:
         out["cpu"] = cpu_optimizer_estimate(torch, steps)
         out["speedup_vs_cpu"] = round(out["cpu"]["muon_plus_shampoo_step_ms"] / out["muon_plus_shampoo_step_ms"], 1)
+        out["soap_speedup_vs_cpu"] = round(out["cpu"]["soap_step_ms"] / out["soap_step_ms"], 1)
     return out
 
 
@@ -300,11 +321,18 @@ def cpu_optimizer_estimate(torch, steps):
     plain = 48 * (t_kron + t_apply) + per_elem * (emb_norms + mlp)
     refresh = plain + 96 * t_root
     shampoo = (2 * refresh + (steps - 2) * plain) / steps
+    t_rot = timed(lambda: oo.two_sided_product(L, sq, L, transpose_a=True))
+    t_eigh = timed(lambda: np.linalg.eigh(L.astype(np.float64)))
+    soap_plain = 48 * (t_kron + 3 * t_rot) + per_elem * (48 * sq.size + emb_norms + mlp)
+    soap_refresh = soap_plain + 96 * t_eigh + 48 * t_rot
+    soap = (soap_refresh + 9 * soap_plain) / 10
     return {"muon_step_ms": round(muon * 1e3, 1), "shampoo_step_ms": round(shampoo * 1e3, 1),
-            "muon_plus_shampoo_step_ms": round((muon + shampoo) * 1e3, 1), "cores": blas_threads(), "kind": "port",
+            "muon_plus_shampoo_step_ms": round((muon + shampoo) * 1e3, 1), "soap_step_ms": round(soap * 1e3, 1),
+            "soap_plain_step_ms": round(soap_plain * 1e3, 1), "cores": blas_threads(), "kind": "port",
             "sample": "numpy oracle: 1 NS5 2048², 1 NS5 2048x8192, 1 kron update + apply 2048², 1 fp64 eigh root "
-                      "2048, AdamW over 2048x8192; scaled by per-step counts (48, 24, 48, 96 per refresh, "
-                      "elements); Shampoo mean = (2 refresh + (steps-2) plain)/steps"}
+                      "2048, 1 rotation Q_Lᵀ·G·Q_R 2048², 1 fp64 eigh 2048, AdamW over 2048x8192; scaled by "
+                      "per-step counts (48, 24, 48, 96 per refresh, 3x48 rotations, elements); Shampoo mean = "
+                      "(2 refresh + (steps-2) plain)/steps, SOAP mean = (refresh + 9 plain)/10"}
 
 
 # ------------------------------------------------------------ HBM traffic

@@ -103,13 +103,27 @@ int pto_precond_apply(const void* L_root, const void* G, const void* R_root, voi
                       int64_t n, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * Two-sided product with optional transposes: out = op(A)*X*op(B),
+ * op(M) = M, or Mᵀ when trans_* is non-zero, associated left to right.
+ * A [m,m], X [m,n], B [n,n], out [m,n]. The reference has no compiled
+ * counterpart: these are SOAP's eigenbasis rotations, Q_Lᵀ*X*Q_R and
+ * Q_L*X*Q_Rᵀ (pytorch_opt/optim/soap.py:123-125, torch matmuls in the
+ * reference), and its second-moment transport (C_L²)ᵀ*v*(C_R²) (:103-107).
+ * pto_precond_apply is the case trans_a = trans_b = 0.
+ */
+size_t pto_two_sided_product_workspace_bytes(int dtype, int64_t m, int64_t n);
+int pto_two_sided_product(const void* A, const void* X, const void* B, void* out, int dtype, int64_t m, int64_t n,
+                          int trans_a, int trans_b, void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * Kernel timing with HIP events. The reference has no counterpart (its
  * StepTimer, pytorch_opt/optim/_common.py:82-98, is host wall-clock). While
  * enabled, every MFMA launch is bracketed by events on its stream;
  * pto_prof_query waits for them and returns the summed milliseconds and
  * launch count for one kernel class ("ns5_gram", "ns5_square",
  * "ns5_update", "kron_left", "kron_right", "gram_update", "root_xmi",
- * "root_pow", "root_mk", "apply_left", "apply_right").
+ * "root_pow", "root_mk", "apply_left", "apply_right", "rotate_left",
+ * "rotate_right").
  */
 int pto_prof_enable(int on);
 int pto_prof_reset(void);

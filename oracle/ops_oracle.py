@@ -22,6 +22,8 @@ Pinning (tests/test_oracle.py):
                        tests/golden when present, else "parity unpinned"
   gram_update          brute-force sum of outer products, clone/EMA/mean
   precond_apply        associativity / brute force in float64
+  two_sided_product    orthogonal round trip Q·(QᵀXQ)·Qᵀ = X, permutation
+                       and sign-flip closed forms, transpose identities
 """
 
 from __future__ import annotations
@@ -177,6 +179,14 @@ def root_residual(X, A, p, damping=0.0):
 def precond_apply(Lr, G, Rr):
     """(L_root·G)·R_root — pytorch_opt/ops/reference.py:117-121."""
     return (np.asarray(Lr) @ np.asarray(G)) @ np.asarray(Rr)
+
+
+def two_sided_product(A, X, B, transpose_a=False, transpose_b=False):
+    """op(A)·X·op(B), left to right — SOAP's rotations and transport,
+    pytorch_opt/optim/soap.py:103-107 (C_L²ᵀ·v·C_R²) and :123-125
+    (Q_Lᵀ·x·Q_R, Q_L·x·Q_Rᵀ)."""
+    A, X, B = np.asarray(A), np.asarray(X), np.asarray(B)
+    return ((_t(A) if transpose_a else A) @ X) @ (_t(B) if transpose_b else B)
 
 
 def gram_update(F, X, beta=0.0, alpha=1.0, append_ones=False, dtype=np.float32):

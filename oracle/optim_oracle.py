@@ -2,10 +2,17 @@
 INFRASTRUCTURE ONLY (used by tests/ and bench.py's cpu_baseline leg).
 
 numpy restatements of one Muon step (pytorch_opt/optim/muon.py:60-102),
-the shared AdamW fallback (pytorch_opt/optim/_common.py:56-79) and one
+the shared AdamW fallback (pytorch_opt/optim/_common.py:56-79), one
 Shampoo step for a single matrix parameter
-(pytorch_opt/optim/shampoo.py:70-160), used for teacher-forced checks:
-given the state a GPU run reached, the oracle computes the next state.
+(pytorch_opt/optim/shampoo.py:70-160) and one SOAP step
+(pytorch_opt/optim/soap.py:48-125), used for teacher-forced checks: given
+the state a GPU run reached, the oracle computes the next state.
+
+Pinning (tests/test_oracle.py): adamw_step against torch.optim.Adam/AdamW;
+soap_matrix_step against the same Adam when the factors stay diagonal (the
+eigenbases are signed permutations, SOAP's analytic identity,
+tests/test_soap.py:8-24 of the reference) and against its own rotation-
+free form when Q_L, Q_R are fixed arbitrary orthogonal matrices.
 """
 
 from __future__ import annotations
@@ -70,3 +77,49 @@ def shampoo_matrix_step(p, g, L, R, L_root, R_root, graft_acc, step, factor_upda
         P = P * np.float32(np.linalg.norm(g2) / (np.linalg.norm(P) + 1e-30))
     p = p - np.float32(lr) * P.reshape(p.shape)
     return p, L, R, L_root, R_root, graft_acc
+
+
+def soap_matrix_step(p, g, state, lr=3e-3, betas=(0.95, 0.95), shampoo_beta=0.95, eps=1e-8,
+                     precondition_frequency=10, weight_decay=0.0):
+    """One SOAP update of a selected matrix (pytorch_opt/optim/soap.py:48-66,
+    :80-125): factor EMA, eigenbasis refresh every `precondition_frequency`
+    steps with the second moment transported through the squared
+    basis-change matrices, then Adam in the eigenbasis.
+
+    `state` holds L, R, exp_avg, exp_avg_sq, step and (after the first
+    refresh) Q_L, Q_R, as numpy arrays; a new dict is returned with p.
+    Eigenvectors come from numpy's eigh (ascending, as torch's): the update
+    is unchanged by the sign of each eigenvector and the transport maps the
+    second moment exactly under such flips, so the oracle need not share
+    the GPU run's eigenvector signs.
+    """
+    st = dict(state)
+    dt = p.dtype
+    g2 = g.reshape(g.shape[0], -1)
+    m, n = g2.shape
+    if "L" not in st:
+        st.update(L=np.zeros((m, m), dt), R=np.zeros((n, n), dt), exp_avg=np.zeros_like(g2),
+                  exp_avg_sq=np.zeros_like(g2), step=0)
+    st["L"], st["R"] = oo.kron_factor_update(st["L"], st["R"], g2, shampoo_beta)
+    if st["step"] % precondition_frequency == 0:
+        QL = np.linalg.eigh(st["L"].astype(np.float64))[1].astype(dt)
+        QR = np.linalg.eigh(st["R"].astype(np.float64))[1].astype(dt)
+        if "Q_L" in st:
+            CL = st["Q_L"].T @ QL
+            CR = st["Q_R"].T @ QR
+            st["exp_avg_sq"] = oo.two_sided_product(CL * CL, st["exp_avg_sq"], CR * CR, transpose_a=True)
+        st["Q_L"], st["Q_R"] = QL, QR
+    QL, QR = st["Q_L"], st["Q_R"]
+    b1, b2 = betas
+    st["step"] += 1
+    t = st["step"]
+    st["exp_avg"] = st["exp_avg"] + dt.type(1 - b1) * (g2 - st["exp_avg"])
+    g_rot = oo.two_sided_product(QL, g2, QR, transpose_a=True)
+    st["exp_avg_sq"] = st["exp_avg_sq"] * dt.type(b2) + dt.type(1 - b2) * g_rot * g_rot
+    m_rot = oo.two_sided_product(QL, st["exp_avg"], QR, transpose_a=True)
+    denom = np.sqrt(st["exp_avg_sq"]) / dt.type((1 - b2 ** t) ** 0.5) + dt.type(eps)
+    upd = oo.two_sided_product(QL, m_rot / denom, QR, transpose_b=True)
+    if weight_decay:
+        p = p * dt.type(1.0 - lr * weight_decay)
+    p = p - dt.type(lr / (1 - b1 ** t)) * upd.reshape(p.shape)
+    return p, st

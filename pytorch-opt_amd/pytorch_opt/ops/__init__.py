@@ -95,6 +95,13 @@ def precond_apply_two_sided(L_root, G, R_root):
     return reference.precond_apply_two_sided(L_root, G, R_root)
 
 
+def two_sided_product(A, X, B, transpose_a=False, transpose_b=False):
+    """op(A)·X·op(B) with op = identity or transpose (SOAP's eigenbasis rotations)."""
+    if _use_native():
+        return _NATIVE.two_sided_product(A, X, B, bool(transpose_a), bool(transpose_b))
+    return reference.two_sided_product(A, X, B, transpose_a=transpose_a, transpose_b=transpose_b)
+
+
 def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
     """F ← beta·F + alpha·X̃ᵀX̃ in place, X̃ = [X, 1] if append_ones (beta=0 overwrites)."""
     if _use_native():
@@ -105,7 +112,7 @@ def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
 
 __all__ = ["get_backend", "set_backend", "native_available", "load_native", "inverse_matrix_root",
            "newton_schulz_orthogonalize", "kron_factor_update_", "precond_apply_two_sided",
-           "gram_update_", "OpsArgumentError", "reference"]
+           "two_sided_product", "gram_update_", "OpsArgumentError", "reference"]
 
 if os.environ.get("PYTORCH_OPT_NATIVE") == "1":
     load_native()

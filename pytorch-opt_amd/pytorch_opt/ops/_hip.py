@@ -48,6 +48,9 @@ SIGNATURES = {
     "pto_precond_apply_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
     "pto_precond_apply": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_size,
                                    _c_ptr]),
+    "pto_two_sided_product_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
+    "pto_two_sided_product": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_int, _c_int,
+                                       _c_ptr, _c_size, _c_ptr]),
     "pto_prof_enable": (_c_int, [_c_int]),
     "pto_prof_reset": (_c_int, []),
     "pto_prof_query": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_c_dbl), ctypes.POINTER(_c_i64)]),
@@ -181,29 +184,42 @@ class HipBackend:
     def precond_apply_two_sided(self, L_root, G, R_root):
         if not (L_root.is_cuda and G.is_cuda and R_root.is_cuda):
             return reference.precond_apply_two_sided(L_root, G, R_root)
-        if L_root.dim() < 2 or G.dim() < 2 or R_root.dim() < 2:
-            raise OpsArgumentError("precond_apply_two_sided expects matrices")
-        m, n = G.shape[-2], G.shape[-1]
-        if L_root.shape[-2:] != (m, m) or R_root.shape[-2:] != (n, n):
-            raise OpsArgumentError(f"precond_apply_two_sided: shapes {tuple(L_root.shape)}, {tuple(G.shape)}, "
-                                   f"{tuple(R_root.shape)} do not chain")
-        out_dtype = torch.promote_types(torch.promote_types(L_root.dtype, G.dtype), R_root.dtype)
+        return self._two_sided(L_root, G, R_root, False, False, "precond_apply_two_sided")
+
+    def two_sided_product(self, A, X, B, transpose_a, transpose_b):
+        if not (A.is_cuda and X.is_cuda and B.is_cuda):
+            return reference.two_sided_product(A, X, B, transpose_a, transpose_b)
+        return self._two_sided(A, X, B, bool(transpose_a), bool(transpose_b), "two_sided_product")
+
+    def _two_sided(self, A, X, B, trans_a, trans_b, what):
+        """op(A)·X·op(B) per matrix of the broadcast batch (square A and B)."""
+        if A.dim() < 2 or X.dim() < 2 or B.dim() < 2:
+            raise OpsArgumentError(f"{what} expects matrices")
+        m, n = X.shape[-2], X.shape[-1]
+        if A.shape[-2:] != (m, m) or B.shape[-2:] != (n, n):
+            raise OpsArgumentError(f"{what}: shapes {tuple(A.shape)}, {tuple(X.shape)}, "
+                                   f"{tuple(B.shape)} do not chain")
+        out_dtype = torch.promote_types(torch.promote_types(A.dtype, X.dtype), B.dtype)
         work = out_dtype if out_dtype in _DTYPE_CODE else torch.float32
-        lead = torch.broadcast_shapes(L_root.shape[:-2], G.shape[:-2], R_root.shape[:-2])
-        Lb = L_root.to(work).expand(*lead, m, m).reshape(-1, m, m)
-        Gb = G.to(work).expand(*lead, m, n).reshape(-1, m, n)
-        Rb = R_root.to(work).expand(*lead, n, n).reshape(-1, n, n)
-        out = torch.empty(Gb.shape, dtype=work, device=G.device)
+        lead = torch.broadcast_shapes(A.shape[:-2], X.shape[:-2], B.shape[:-2])
+        Ab = A.to(work).expand(*lead, m, m).reshape(-1, m, m)
+        Xb = X.to(work).expand(*lead, m, n).reshape(-1, m, n)
+        Bb = B.to(work).expand(*lead, n, n).reshape(-1, n, n)
+        out = torch.empty(Xb.shape, dtype=work, device=X.device)
         code = _DTYPE_CODE[work]
-        with torch.cuda.device(G.device):
-            nbytes = self._lib.pto_precond_apply_workspace_bytes(code, m, n)
-            ws = self._workspace(nbytes, G.device)
-            stream = self._stream(G.device)
+        with torch.cuda.device(X.device):
+            nbytes = self._lib.pto_two_sided_product_workspace_bytes(code, m, n)
+            ws = self._workspace(nbytes, X.device)
+            stream = self._stream(X.device)
             for i in range(out.shape[0]):
-                Li, Gi, Ri = Lb[i].contiguous(), Gb[i].contiguous(), Rb[i].contiguous()
-                rc = self._lib.pto_precond_apply(_ptr(Li), _ptr(Gi), _ptr(Ri), _ptr(out[i]), code, m, n,
-                                                 _ptr(ws), nbytes, stream)
-                self._check(rc, "precond_apply_two_sided")
+                Ai, Xi, Bi = Ab[i].contiguous(), Xb[i].contiguous(), Bb[i].contiguous()
+                if trans_a or trans_b:
+                    rc = self._lib.pto_two_sided_product(_ptr(Ai), _ptr(Xi), _ptr(Bi), _ptr(out[i]), code, m, n,
+                                                         int(trans_a), int(trans_b), _ptr(ws), nbytes, stream)
+                else:
+                    rc = self._lib.pto_precond_apply(_ptr(Ai), _ptr(Xi), _ptr(Bi), _ptr(out[i]), code, m, n,
+                                                     _ptr(ws), nbytes, stream)
+                self._check(rc, what)
         out = out.reshape(*lead, m, n)
         return out if out.dtype == out_dtype else out.to(out_dtype)
 

@@ -145,6 +145,17 @@ def precond_apply_two_sided(L_root, G, R_root):
     return L_root @ G @ R_root
 
 
+def two_sided_product(A, X, B, transpose_a=False, transpose_b=False):
+    """op(A)·X·op(B), op = identity or transpose, associated left to right.
+
+    SOAP's rotations into and out of the Shampoo eigenbasis, Q_Lᵀ·X·Q_R and
+    Q_L·X·Q_Rᵀ (optim/soap.py:123-125), and its second-moment transport
+    (C_L²)ᵀ·v·(C_R²) (:103-107), exposed as an op so a compiled backend can
+    serve them. precond_apply_two_sided is the case without transposes.
+    """
+    return (A.mT if transpose_a else A) @ X @ (B.mT if transpose_b else B)
+
+
 def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
     """In place: F ← β·F + α·X̃ᵀX̃ with X̃ = [X, 1] if append_ones; β = 0 overwrites.
 

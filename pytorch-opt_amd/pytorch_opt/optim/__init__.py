@@ -1,5 +1,6 @@
 from .muon import Muon
 from .routing import matrix_param_groups
 from .shampoo import Shampoo
+from .soap import SOAP
 
-__all__ = ["Muon", "Shampoo", "matrix_param_groups"]
+__all__ = ["Muon", "Shampoo", "SOAP", "matrix_param_groups"]

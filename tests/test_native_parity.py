@@ -291,6 +291,35 @@ def test_apply_vs_oracle(native_backend, shape):
     assert _relfro(_np(got), want) <= 1e-5
 
 
+@pytest.mark.parametrize("trans", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("shape", [(4, 7), (96, 200), (300, 70), (256, 384)])
+def test_two_sided_product_vs_oracle(native_backend, trans, shape):
+    """op(A)·X·op(B) in fp32 against the float64 oracle; (256, 384) takes the
+    unpacked operand path for whichever factor is read as stored."""
+    m, n = shape
+    A, X, B = torch.randn(m, m), torch.randn(m, n), torch.randn(n, n)
+    got = ops.two_sided_product(A.to(DEV), X.to(DEV), B.to(DEV), *trans)
+    want = oo.two_sided_product(A.double().numpy(), X.double().numpy(), B.double().numpy(), *trans)
+    assert _relfro(_np(got), want) <= 1e-5
+
+
+def test_two_sided_product_fp64_bf16_and_rotation(native_backend):
+    A, X, B = (torch.randn(s, dtype=torch.float64) for s in [(70, 70), (70, 130), (130, 130)])
+    got = ops.two_sided_product(A.to(DEV), X.to(DEV), B.to(DEV), True, True)
+    assert torch.allclose(got.cpu(), A.T @ X @ B.T, atol=1e-10)
+    Xb = torch.randn(128, 256).bfloat16()
+    Ab, Bb = torch.randn(128, 128).bfloat16(), torch.randn(256, 256).bfloat16()
+    got = ops.two_sided_product(Ab.to(DEV), Xb.to(DEV), Bb.to(DEV), True, False)
+    want = oo.two_sided_product(Ab.double().numpy(), Xb.double().numpy(), Bb.double().numpy(), True, False)
+    assert _relfro(_np(got), want) <= 2e-2
+    # an eigenbasis round trip Q·(QᵀXQ')·Q'ᵀ = X
+    QL = torch.linalg.qr(torch.randn(300, 300, dtype=torch.float64))[0].float().to(DEV)
+    QR = torch.linalg.qr(torch.randn(200, 200, dtype=torch.float64))[0].float().to(DEV)
+    X = torch.randn(300, 200, device=DEV)
+    back = ops.two_sided_product(QL, ops.two_sided_product(QL, X, QR, True, False), QR, False, True)
+    assert _relfro(_np(back), _np(X)) <= 1e-5
+
+
 def test_apply_batched_and_promoted(native_backend):
     Lr = torch.randn(2, 5, 5, dtype=torch.float64)
     G = torch.randn(2, 5, 3, dtype=torch.float64)

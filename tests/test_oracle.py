@@ -203,3 +203,96 @@ def test_precond_apply_brute_force():
     L, G, R = rng.standard_normal((4, 4)), rng.standard_normal((4, 7)), rng.standard_normal((7, 7))
     want = np.einsum("ij,jk,kl->il", L, G, R)
     np.testing.assert_allclose(oo.precond_apply(L, G, R), want, atol=1e-12)
+
+
+def test_two_sided_product_closed_forms():
+    """Orthogonal round trip, permutation/sign closed form, transposes."""
+    rng = np.random.default_rng(21)
+    m, n = 7, 5
+    QL, QR = _orth(m, rng), _orth(n, rng)
+    X = rng.standard_normal((m, n))
+    rot = oo.two_sided_product(QL, X, QR, transpose_a=True)
+    np.testing.assert_allclose(oo.two_sided_product(QL, rot, QR, transpose_b=True), X, atol=1e-12)
+    # signed permutations: (PᵀXS)[i, j] = sign·X[perm_L[i], perm_R[j]]
+    pl, pr = rng.permutation(m), rng.permutation(n)
+    sl, sr = rng.choice([-1.0, 1.0], m), rng.choice([-1.0, 1.0], n)
+    PL = np.zeros((m, m)); PL[pl, np.arange(m)] = sl
+    PR = np.zeros((n, n)); PR[pr, np.arange(n)] = sr
+    want = X[pl][:, pr] * sl[:, None] * sr[None, :]
+    np.testing.assert_allclose(oo.two_sided_product(PL, X, PR, transpose_a=True), want, atol=1e-14)
+    # each flag transposes exactly its own factor
+    A, B = rng.standard_normal((m, m)), rng.standard_normal((n, n))
+    for ta in (False, True):
+        for tb in (False, True):
+            got = oo.two_sided_product(A, X, B, ta, tb)
+            np.testing.assert_allclose(got, (A.T if ta else A) @ X @ (B.T if tb else B), atol=1e-12)
+    assert not np.allclose(oo.two_sided_product(A, X, B, True, False), oo.two_sided_product(A, X, B, False, False))
+
+
+def test_adamw_oracle_matches_torch():
+    import torch
+
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(22)
+    p0 = rng.standard_normal((6, 4)).astype(np.float32)
+    for wd in (0.0, 0.1):
+        pt = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+        opt = torch.optim.AdamW([pt], lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=wd)
+        p, m, v = p0.copy(), np.zeros_like(p0), np.zeros_like(p0)
+        for t in range(1, 6):
+            g = rng.standard_normal(p0.shape).astype(np.float32)
+            pt.grad = torch.from_numpy(g.copy())
+            opt.step()
+            p, m, v = oopt.adamw_step(p, g, m, v, t, 1e-2, (0.9, 0.95), 1e-8, wd)
+        np.testing.assert_allclose(p, pt.detach().numpy(), atol=1e-6)
+
+
+def _torch_adam_path(p0, grads, lr, betas, eps):
+    import torch
+
+    pt = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+    opt = torch.optim.Adam([pt], lr=lr, betas=betas, eps=eps)
+    for g in grads:
+        pt.grad = torch.from_numpy(g.copy())
+        opt.step()
+    return pt.detach().numpy()
+
+
+def test_soap_oracle_is_adam_for_diagonal_factors():
+    """Diagonal gradients keep L and R diagonal, the eigenbases are signed
+    permutations and SOAP is exactly Adam (the reference's analytic test,
+    tests/test_soap.py:8-24)."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(23)
+    p0 = rng.standard_normal((5, 5)).astype(np.float32)
+    grads = [np.diag(rng.standard_normal(5)).astype(np.float32) for _ in range(7)]
+    p, st = p0.copy(), {}
+    for g in grads:
+        p, st = oopt.soap_matrix_step(p, g, st, lr=1e-2, betas=(0.9, 0.999), precondition_frequency=2)
+    np.testing.assert_allclose(p, _torch_adam_path(p0, grads, 1e-2, (0.9, 0.999), 1e-8), atol=1e-6)
+
+
+def test_soap_oracle_fixed_basis_is_rotated_adam():
+    """With the basis fixed after the first refresh, SOAP is Adam run on the
+    rotated gradients Q_Lᵀ·G·Q_R, rotated back: p = p0 + Q_L·z·Q_Rᵀ where z
+    is Adam's displacement. A transposed rotation fails this."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(24)
+    m, n = 6, 4
+    p0 = rng.standard_normal((m, n)).astype(np.float64)
+    grads = [rng.standard_normal((m, n)) for _ in range(5)]
+    p, st = p0.copy(), {}
+    p, st = oopt.soap_matrix_step(p, grads[0], st, lr=1e-2, precondition_frequency=1000)
+    QL, QR = st["Q_L"], st["Q_R"]
+    for g in grads[1:]:
+        p, st = oopt.soap_matrix_step(p, g, st, lr=1e-2, precondition_frequency=1000)
+    rot = [QL.T @ g @ QR for g in grads]
+    z = _torch_adam_path(np.zeros((m, n)), rot, 1e-2, (0.95, 0.95), 1e-8)
+    np.testing.assert_allclose(p, p0 + QL @ z @ QR.T, atol=1e-10)
+    # the planted slip (un-transposed left rotation) is caught
+    bad = [QL @ g @ QR for g in grads]
+    z_bad = _torch_adam_path(np.zeros((m, n)), bad, 1e-2, (0.95, 0.95), 1e-8)
+    assert not np.allclose(p, p0 + QL @ z_bad @ QR.T, atol=1e-4)
