@@ -116,6 +116,22 @@ int pto_two_sided_product(const void* A, const void* X, const void* B, void* out
                           int trans_a, int trans_b, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * One AdamW step of a dense tensor, in place: the shared fallback of the
+ * optimizers, pytorch_opt/optim/_common.py:56-79 (torch elementwise ops in
+ * the reference; no compiled counterpart). With bc1 = 1 - beta1^step and
+ * bc2 = 1 - beta2^step:
+ *   m <- lerp(m, g, 1 - beta1);  v <- beta2*v + (1 - beta2)*g*g;
+ *   u <- (m / bc1) / (sqrt(v) / bc2^0.5 + eps);  p <- p*(1 - lr*wd) - lr*u
+ * each op rounded to the tensor dtype in that order. p, g, m, v hold n
+ * elements of `dtype`. update_sq (device pointer, may be NULL) receives the
+ * sum of u^2 in double (the Muon diagnostic, pytorch_opt/optim/muon.py:97).
+ */
+size_t pto_adamw_workspace_bytes(void);
+int pto_adamw_step(void* p, const void* g, void* m, void* v, int dtype, int64_t n, double lr, double weight_decay,
+                   double beta1, double beta2, double eps, int64_t step, double* update_sq, void* workspace,
+                   size_t ws_bytes, void* stream);
+
+/*
  * Kernel timing with HIP events. The reference has no counterpart (its
  * StepTimer, pytorch_opt/optim/_common.py:82-98, is host wall-clock). While
  * enabled, every MFMA launch is bracketed by events on its stream;

@@ -10,7 +10,9 @@ Backends (the same switch as the reference's pytorch_opt/ops/__init__.py:16-88):
 ``load_native()`` loads the prebuilt library; like the reference it never
 raises (it warns and returns False). ``PYTORCH_OPT_NATIVE=1`` at import
 calls it. Op signatures and defaults are the reference's
-(pytorch_opt/ops/__init__.py:58-84); ``gram_update_`` is additive.
+(pytorch_opt/ops/__init__.py:58-84); ``gram_update_`` (K-FAC factor
+statistics), ``two_sided_product`` (SOAP's rotations) and ``adamw_step_``
+(the optimizers' shared AdamW fallback) are additive.
 """
 
 from __future__ import annotations
@@ -102,6 +104,17 @@ def two_sided_product(A, X, B, transpose_a=False, transpose_b=False):
     return reference.two_sided_product(A, X, B, transpose_a=transpose_a, transpose_b=transpose_b)
 
 
+def adamw_step_(p, grad, exp_avg, exp_avg_sq, lr, weight_decay, betas, eps, step, return_update_sq=False):
+    """One fused AdamW step in place (the optimizers' shared fallback); `step` is
+    the already-incremented count. Returns Σ update² as a 0-dim tensor if asked."""
+    if _use_native():
+        b1, b2 = betas
+        return _NATIVE.adamw_step_(p, grad, exp_avg, exp_avg_sq, float(lr), float(weight_decay), float(b1),
+                                   float(b2), float(eps), int(step), bool(return_update_sq))
+    return reference.adamw_step_(p, grad, exp_avg, exp_avg_sq, lr, weight_decay, betas, eps, step,
+                                 return_update_sq=return_update_sq)
+
+
 def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
     """F ← beta·F + alpha·X̃ᵀX̃ in place, X̃ = [X, 1] if append_ones (beta=0 overwrites)."""
     if _use_native():
@@ -112,7 +125,7 @@ def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
 
 __all__ = ["get_backend", "set_backend", "native_available", "load_native", "inverse_matrix_root",
            "newton_schulz_orthogonalize", "kron_factor_update_", "precond_apply_two_sided",
-           "two_sided_product", "gram_update_", "OpsArgumentError", "reference"]
+           "two_sided_product", "gram_update_", "adamw_step_", "OpsArgumentError", "reference"]
 
 if os.environ.get("PYTORCH_OPT_NATIVE") == "1":
     load_native()

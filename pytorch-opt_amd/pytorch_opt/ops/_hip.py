@@ -51,6 +51,9 @@ SIGNATURES = {
     "pto_two_sided_product_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
     "pto_two_sided_product": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_int, _c_int,
                                        _c_ptr, _c_size, _c_ptr]),
+    "pto_adamw_workspace_bytes": (_c_size, []),
+    "pto_adamw_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_dbl, _c_dbl, _c_dbl,
+                                _c_dbl, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "pto_prof_enable": (_c_int, [_c_int]),
     "pto_prof_reset": (_c_int, []),
     "pto_prof_query": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_c_dbl), ctypes.POINTER(_c_i64)]),
@@ -222,6 +225,32 @@ class HipBackend:
                 self._check(rc, what)
         out = out.reshape(*lead, m, n)
         return out if out.dtype == out_dtype else out.to(out_dtype)
+
+    def adamw_step_(self, p, g, m, v, lr, weight_decay, beta1, beta2, eps, step, return_update_sq):
+        tensors = (p, g, m, v)
+        if not all(t.is_cuda for t in tensors):
+            return reference.adamw_step_(p, g, m, v, lr, weight_decay, (beta1, beta2), eps, step, return_update_sq)
+        if any(t.shape != p.shape or t.dtype != p.dtype for t in tensors):
+            raise OpsArgumentError("adamw_step_: p, grad and both moments must share shape and dtype")
+        if p.dtype not in _DTYPE_CODE:
+            # float16 has no kernel here: torch's own elementwise ops, on the GPU, in the reference's order
+            return reference.adamw_step_(p, g, m, v, lr, weight_decay, (beta1, beta2), eps, step, return_update_sq)
+        work = [t if t.is_contiguous() else t.contiguous() for t in tensors]
+        sq = torch.empty((), dtype=torch.float64, device=p.device) if return_update_sq else None
+        with torch.cuda.device(p.device):
+            nbytes = self._lib.pto_adamw_workspace_bytes()
+            ws = self._workspace(nbytes, p.device) if return_update_sq else None
+            rc = self._lib.pto_adamw_step(_ptr(work[0]), _ptr(work[1]), _ptr(work[2]), _ptr(work[3]),
+                                          _DTYPE_CODE[p.dtype], p.numel(), float(lr), float(weight_decay),
+                                          float(beta1), float(beta2), float(eps), int(step),
+                                          _ptr(sq) if sq is not None else None,
+                                          _ptr(ws) if ws is not None else None, nbytes if ws is not None else 0,
+                                          self._stream(p.device))
+        self._check(rc, "adamw_step_")
+        for dst, src in zip((p, m, v), (work[0], work[2], work[3])):
+            if dst is not src:
+                dst.copy_(src)
+        return sq
 
     def gram_update_(self, F, X, beta, alpha, append_ones):
         if not (F.is_cuda and X.is_cuda):

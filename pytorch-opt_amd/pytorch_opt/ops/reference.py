@@ -145,6 +145,21 @@ def precond_apply_two_sided(L_root, G, R_root):
     return L_root @ G @ R_root
 
 
+def adamw_step_(p, grad, exp_avg, exp_avg_sq, lr, weight_decay, betas, eps, step, return_update_sq=False):
+    """One AdamW step in place, the optimizers' shared fallback
+    (optim/_common.py:56-79) from the moment updates on; `step` is the
+    already-incremented step count. Returns Σ update² (a 0-dim tensor) when
+    asked, else None."""
+    b1, b2 = betas
+    exp_avg.lerp_(grad, 1 - b1)
+    exp_avg_sq.mul_(b2).addcmul_(grad, grad, value=1 - b2)
+    bc1, bc2 = 1 - b1 ** step, 1 - b2 ** step
+    denom = (exp_avg_sq.sqrt() / bc2 ** 0.5).add_(eps)
+    update = (exp_avg / bc1) / denom
+    p.mul_(1 - lr * weight_decay).add_(update, alpha=-lr)
+    return update.pow(2).sum() if return_update_sq else None
+
+
 def two_sided_product(A, X, B, transpose_a=False, transpose_b=False):
     """op(A)·X·op(B), op = identity or transpose, associated left to right.
 

@@ -127,8 +127,8 @@ class Muon(Optimizer, DiagnosticsMixin):
                         contrib.append(None)
                     else:
                         n_adamw += 1
-                        upd, lr_eff = adamw_update(p, g, st, group)
-                        contrib.append((upd.pow(2).sum(), lr_eff, upd.numel()))
+                        sq, lr_eff = adamw_update(p, g, st, group, want_update_sq=True)
+                        contrib.append((sq, lr_eff, p.numel()))
                 for items in buckets.values():
                     self._orthogonalize_bucket(group, items, contrib)
             sq_sum, count = 0.0, 0
