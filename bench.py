@@ -18,7 +18,9 @@ same workload, and secondary figures:
   optimizer     Muon + Shampoo steps on the synthetic 12-layer d=2048
                 parameter set (40 steps each), SOAP on its 48 attention
                 matrices (one refresh period, 10 steps), with the CPU
-                oracle's per-step estimate from a bounded sample.
+                oracle's per-step estimate from a bounded sample;
+  kfac          K-FAC and EKFAC steps on 4 x Linear(2048, 2048), 8192
+                tokens (one inv_every = 10 period), with a CPU estimate.
 """
 
 from __future__ import annotations
@@ -335,6 +337,66 @@ def cpu_optimizer_estimate(torch, steps):
                       "(2 refresh + (steps-2) plain)/steps, SOAP mean = (refresh + 9 plain)/10"}
 
 
+# ------------------------------------------------------------ K-FAC / EKFAC
+
+KFAC_D, KFAC_DEPTH, KFAC_TOKENS = 2048, 4, 8192
+
+
+def bench_kfac(torch, dev, cpu):
+    """K-FAC and EKFAC optimizer steps on 4 x Linear(2048, 2048) with bias,
+    8192 tokens, fp32, over one inv_every = 10 period: step 0 refreshes the
+    8 damped inverses / eigenbases (float64 eigh of 2049² and 2048², batched),
+    steps 1-9 only precondition (two MFMA products per layer) and update.
+    The backward-hook factor statistics are outside opt.step() and are timed
+    by the K-FAC Gram line of `factors`."""
+    from pytorch_opt import EKFAC, KFAC
+
+    d, depth, tokens = KFAC_D, KFAC_DEPTH, KFAC_TOKENS
+    flops = depth * (2 * d * d * (d + 1) + 2 * d * (d + 1) * (d + 1))  # iG·V, (iG·V)·iA per layer
+    out = {"workload": f"{depth} x Linear({d}, {d}) + bias, {tokens} tokens, fp32, inv_every 10"}
+    for name, cls in (("kfac", KFAC), ("ekfac", EKFAC)):
+        torch.manual_seed(7)
+        model = torch.nn.Sequential(*[torch.nn.Linear(d, d) for _ in range(depth)]).to(dev)
+        opt = cls(model, lr=1e-3, damping=1e-3, inv_every=10)
+        X = torch.randn(tokens, d, device=dev)
+        per = []
+        for _ in range(10):
+            opt.zero_grad(set_to_none=True)
+            (0.5 * model(X).pow(2).sum() / tokens).backward()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            opt.step()
+            torch.cuda.synchronize()
+            per.append(time.perf_counter() - t0)
+        plain = sum(per[1:]) / 9
+        out[name] = {"refresh_step_ms": round(per[0] * 1e3, 1), "plain_step_ms": round(plain * 1e3, 2),
+                     "mean_step_ms": round(sum(per) / 10 * 1e3, 2)}
+        if name == "kfac":
+            out[name]["plain_alg_tflops"] = round(flops / plain / 1e12, 2)
+        del model, opt, X
+        torch.cuda.empty_cache()
+    if cpu:
+        import numpy as np
+
+        from oracle import ops_oracle as oo
+
+        rng = np.random.default_rng(1)
+        A = rng.standard_normal((d + 1, d + 1)).astype(np.float32)
+        G = rng.standard_normal((d, d)).astype(np.float32)
+        V = rng.standard_normal((d, d + 1)).astype(np.float32)
+        t_apply = timed(lambda: oo.precond_apply(G, V, A))
+        t_eigh = timed(lambda: np.linalg.eigh(A.astype(np.float64) @ A.T.astype(np.float64)))
+        plain_c = depth * t_apply
+        refresh_c = plain_c + 2 * depth * t_eigh
+        out["cpu"] = {"kfac_plain_step_ms": round(plain_c * 1e3, 1), "kfac_refresh_step_ms": round(refresh_c * 1e3, 1),
+                      "kfac_mean_step_ms": round((refresh_c + 9 * plain_c) / 10 * 1e3, 1), "cores": blas_threads(),
+                      "kind": "port",
+                      "sample": "numpy oracle: one (G·V)·A product of 2048x2049 and one float64 eigh of 2049², "
+                                "scaled by 4 layers (and 8 eighs per refresh); mean over one 10-step period"}
+        out["kfac_speedup_vs_cpu"] = round(out["cpu"]["kfac_mean_step_ms"] / out["kfac"]["mean_step_ms"], 1)
+    return out
+
+
 # ------------------------------------------------------------ HBM traffic
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ns5_bf16_traffic.json")
@@ -502,6 +564,7 @@ def main():
         line["factors"] = bench_factors(torch, ops, hip, dev, cpu)
         line["roots"] = bench_roots(torch, hip, dev, cpu)
         line["optimizer"] = bench_optimizer(torch, ops, hip, dev, args.opt_steps, cpu)
+        line["kfac"] = bench_kfac(torch, dev, cpu)
     print(json.dumps(line))
 
 

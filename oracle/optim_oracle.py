@@ -123,3 +123,34 @@ def soap_matrix_step(p, g, state, lr=3e-3, betas=(0.95, 0.95), shampoo_beta=0.95
         p = p * dt.type(1.0 - lr * weight_decay)
     p = p - dt.type(lr / (1 - b1 ** t)) * upd.reshape(p.shape)
     return p, st
+
+
+def kfac_damping(A, G, damping):
+    """π-split of Tikhonov damping, pytorch_opt/curvature/damping.py:10-26:
+    γ_A = π√λ, γ_G = √λ/π, π = √(mean diag A / mean diag G) (1 if not positive)."""
+    nu_a = float(np.trace(A)) / A.shape[-1]
+    nu_g = float(np.trace(G)) / G.shape[-1]
+    ok = np.isfinite(nu_a) and np.isfinite(nu_g) and nu_a > 0 and nu_g > 0
+    pi = float(np.sqrt(nu_a / nu_g)) if ok else 1.0
+    r = float(np.sqrt(damping))
+    return pi * r, r / pi
+
+
+def kfac_direction(V, A, G, damping):
+    """K-FAC natural gradient of one module (pytorch_opt/optim/kfac.py:130-142,
+    145-154): (G + γ_G I)⁻¹·V·(A + γ_A I)⁻¹, by two linear solves in float64."""
+    V, A, G = (np.asarray(x, np.float64) for x in (V, A, G))
+    ga, gg = kfac_damping(A, G, damping)
+    left = np.linalg.solve(G + gg * np.eye(G.shape[0]), V)
+    return np.linalg.solve((A + ga * np.eye(A.shape[0])).T, left.T).T
+
+
+def ekfac_direction(V, QA, QG, s_prev, scale_decay, damping):
+    """EKFAC direction (pytorch_opt/optim/ekfac.py:44-58) given the previous
+    scales s_prev (None on the first call): Vt = Q_Gᵀ·V·Q_A,
+    s = decay·s_prev + (1 − decay)·Vt², d = Q_G·(Vt / (s + λ))·Q_Aᵀ.
+    Returns (d, s)."""
+    V, QA, QG = (np.asarray(x, np.float64) for x in (V, QA, QG))
+    Vt = oo.two_sided_product(QG, V, QA, transpose_a=True)
+    s = Vt * Vt if s_prev is None else scale_decay * np.asarray(s_prev, np.float64) + (1 - scale_decay) * Vt * Vt
+    return oo.two_sided_product(QG, Vt / (s + damping), QA, transpose_b=True), s

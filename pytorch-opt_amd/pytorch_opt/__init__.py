@@ -2,15 +2,15 @@
 
 Drop-in for the reference package's ``pytorch_opt.ops`` hot path and the
 optimizers that drive it (Muon, Shampoo, the shared AdamW fallback and
-routing, and the K-FAC factor tracker), plus SOAP, whose eigenbasis
-rotations run on the same kernels. ``pytorch_opt.ops.load_native()``
-loads the gfx950 HIP library.
+routing, and the K-FAC factor tracker), plus SOAP, K-FAC and EKFAC, whose
+rotations and preconditioner products run on the same kernels.
+``pytorch_opt.ops.load_native()`` loads the gfx950 HIP library.
 """
 
 from . import ops
 from .curvature import KronTracker
-from .optim import SOAP, Muon, Shampoo, matrix_param_groups
+from .optim import EKFAC, KFAC, SOAP, Muon, Shampoo, matrix_param_groups
 
 __version__ = "0.1.0"
 
-__all__ = ["ops", "Muon", "Shampoo", "SOAP", "matrix_param_groups", "KronTracker", "__version__"]
+__all__ = ["ops", "Muon", "Shampoo", "SOAP", "KFAC", "EKFAC", "matrix_param_groups", "KronTracker", "__version__"]

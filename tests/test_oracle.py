@@ -296,3 +296,41 @@ def test_soap_oracle_fixed_basis_is_rotated_adam():
     bad = [QL @ g @ QR for g in grads]
     z_bad = _torch_adam_path(np.zeros((m, n)), bad, 1e-2, (0.95, 0.95), 1e-8)
     assert not np.allclose(p, p0 + QL @ z_bad @ QR.T, atol=1e-4)
+
+
+def test_kfac_direction_is_the_dense_kronecker_solve():
+    """vec(G⁻¹·V·A⁻¹) = (A ⊗ G)⁻¹·vec(V) with column-major vec (the
+    reference's orientation test, tests/test_kfac.py:9-20); the swapped
+    Kronecker order (a plausible slip) does not match."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(31)
+    m, n = 4, 6
+    V = rng.standard_normal((m, n))
+    Xa, Xg = rng.standard_normal((n, 3 * n)), rng.standard_normal((m, 3 * m))
+    A, G = Xa @ Xa.T / n, Xg @ Xg.T / m
+    ga, gg = oopt.kfac_damping(A, G, 1e-2)
+    Ad, Gd = A + ga * np.eye(n), G + gg * np.eye(m)
+    vec = lambda M: M.T.reshape(-1)  # noqa: E731
+    want = np.linalg.solve(np.kron(Ad, Gd), vec(V)).reshape(n, m).T
+    np.testing.assert_allclose(oopt.kfac_direction(V, A, G, 1e-2), want, atol=1e-12)
+    swapped = np.linalg.solve(np.kron(Gd, Ad), vec(V)).reshape(n, m).T  # factors swapped, same vec
+    assert not np.allclose(swapped, want, atol=1e-6)
+    # π-split: γ_A·γ_G = damping and γ_A/γ_G = mean diag A / mean diag G
+    assert np.isclose(ga * gg, 1e-2) and np.isclose(ga / gg, (np.trace(A) / n) / (np.trace(G) / m))
+
+
+def test_ekfac_direction_with_eigenvalue_scales_is_kfac():
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(32)
+    m, n = 5, 3
+    V = rng.standard_normal((m, n))
+    Xa, Xg = rng.standard_normal((n, 2 * n)), rng.standard_normal((m, 2 * m))
+    A, G = Xa @ Xa.T, Xg @ Xg.T
+    evA, QA = np.linalg.eigh(A)
+    evG, QG = np.linalg.eigh(G)
+    d, s = oopt.ekfac_direction(V, QA, QG, np.outer(evG, evA), 1.0, 0.0)
+    np.testing.assert_allclose(d, np.linalg.solve(G, V) @ np.linalg.inv(A), rtol=1e-9, atol=1e-12)
+    d0, s0 = oopt.ekfac_direction(V, QA, QG, None, 0.9, 1e-3)
+    np.testing.assert_allclose(s0, (QG.T @ V @ QA) ** 2, atol=1e-14)
