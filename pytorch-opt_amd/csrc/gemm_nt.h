@@ -218,7 +218,11 @@ struct LdsPlan {
   static constexpr int ARR = ((STAGE > EPI ? STAGE : EPI) + 15) / 16 * 16;
 };
 
-template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false>
+// PT: P is stored [K][M] (M contiguous) and read like a QN operand. For a
+// symmetric P (B' in X' = B'·X, A in A·A) that is P itself: its rows are
+// its columns, so the product reads it with conflict-free transposing LDS
+// reads and 512-byte DMA rows instead of 16-byte row chunks.
+template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false>
 __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   typedef Mfma<T> MF;
   typedef typename MF::cvec_t cvec_t;
@@ -235,14 +239,19 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   constexpr int IPW = (BM + BN) / 16 / NW;         // DMA instructions per wave per tile
   constexpr int QRB = QN ? BN * (int)sizeof(T) : kRowBytes;  // bytes per Q row in LDS
   constexpr int CPR = QRB / 16;                    // 16-byte chunks per Q row
+  constexpr int PRB = PT ? BM * (int)sizeof(T) : kRowBytes;  // bytes per P row in LDS
+  constexpr int CPRP = PRB / 16;                   // 16-byte chunks per P row
   static_assert((BM + BN) % (16 * NW) == 0 && IPW >= 1, "DMA split");
+  static_assert(!PT || (QN && CPRP >= 16 && 1024 % PRB == 0),
+                "PT layout: with QN, P rows of 256 bytes or more dividing 1 KiB");
   static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0 && WTM % 16 == 0, "wave tile");
   static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
   static_assert(3 * IPW <= 63, "vmcnt range");
   static_assert(Plan::RPP % MF::MN == 0 && WTM % Plan::RPP == 0, "epilogue passes");
   static_assert(kStages * Plan::ARR <= Plan::kLdsMax, "LDS budget");
-  static_assert(!QN || (sizeof(T) == 2 && !UPPER && CPR >= 16 && 1024 % QRB == 0 && (BM * kRowBytes) % 1024 == 0),
-                "QN layout: bf16 full products, Q rows of 256 bytes or more");
+  static_assert(!QN || (sizeof(T) == 2 && (!UPPER || PT) && CPR >= 16 && 1024 % QRB == 0 &&
+                        (BM * kRowBytes) % 1024 == 0),
+                "QN layout: bf16, Q rows of 256 bytes or more; symmetric products only with PT");
 
   if (g.guard != nullptr && *g.guard != 0) return;
 
@@ -270,7 +279,8 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // (L%4) ^ swz(row); rows past M (N) re-read the last valid row. In the
   // QN layout a Q lane supplies row rq = byte offset / QRB, physical chunk
   // L % CPR, logical chunk (L % CPR) ^ swzq(rq); columns past the row
-  // pitch re-read its last chunk.
+  // pitch re-read its last chunk. A PT lane does the same in the P region
+  // (rows of PRB bytes, columns from row0).
   const char* src[IPW];
   unsigned step[IPW];  // bytes between consecutive K tiles (the launcher bounds it)
   int dst_off[IPW];
@@ -279,7 +289,13 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     const int R0 = 16 * (wave * IPW + q), r = R0 + (lane >> 2);
     const int chunk = (lane & 3) ^ swz(r);
     const T* s;
-    if (R0 < BM) {
+    if (PT && R0 < BM) {
+      const int rp = R0 * kRowBytes / PRB + lane / CPRP;
+      const int c = (lane % CPRP) ^ swzq(rp);
+      const int64_t col = min((int64_t)row0 + c * VEC, g.ldp - VEC);
+      s = static_cast<const T*>(g.P) + (int64_t)b * g.sP + (int64_t)rp * g.ldp + col;
+      step[q] = (unsigned)(kRowBytes * g.ldp);
+    } else if (R0 < BM) {
       const int gr = min(row0 + r, max(g.M - 1, 0));
       s = static_cast<const T*>(g.P) + (int64_t)b * g.sP + (int64_t)gr * g.ldp + chunk * VEC;
       step[q] = kRowBytes;
@@ -328,12 +344,21 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       qoff[fn] = qr * QRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
     }
   }
+  int poff[FM];  // PT: the same for fragment fm of P (columns = rows of the output)
+  if constexpr (PT) {
+    const int li = lane & 15, qr = KSPAN * lg + (li >> 2);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int col = wm * WTM + fm * MF::MN + (lane & (MF::MN - 1) & ~15) + 4 * (li & 3);
+      poff[fm] = qr * PRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
+    }
+  }
   // One K tile's MFMA operands for this wave.
   struct Frag {
     uint4 a[NRG][FM], b[NRG][FN];
   };
   constexpr int kTileMfma = NRG * IPR * FM * FN;              // MFMAs per K tile
-  constexpr int kFragReads = NRG * (FM + (QN ? 2 : 1) * FN);  // LDS reads per K tile
+  constexpr int kFragReads = NRG * ((PT ? 2 : 1) * FM + (QN ? 2 : 1) * FN);  // LDS reads per K tile
   static_assert(kTileMfma % IPW == 0 && kFragReads % IPW == 0, "schedule groups");
   // Order within a step: LDS reads for the next tile all first, or spread
   // between the MFMA groups (measured faster for the QN layout, slower for
@@ -344,9 +369,20 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 #pragma unroll
     for (int rg = 0; rg < NRG; ++rg) {
       const int off = ((lg * NRG + rg) ^ sw) * 16;
+      if constexpr (PT) {
+        const char* Ps = stage + 8 * rg * PRB;
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
-        f.a[rg][fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
+        for (int fm = 0; fm < FM; ++fm) {
+          v4i16_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(Ps + poff[fm]));
+          v4i16_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(Ps + poff[fm] + 4 * PRB));
+          uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+          f.a[rg][fm] = make_uint4(l2.x, l2.y, h2.x, h2.y);
+        }
+      } else {
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+          f.a[rg][fm] = *reinterpret_cast<const uint4*>(Pw + fm * MF::MN * kRowBytes + off);
+      }
       if constexpr (QN) {
         // lanes of k-group lg, step rg: k = KSPAN*lg + 8*rg + 0..7
         const char* Qs = stage + BM * kRowBytes + 8 * rg * QRB;
@@ -603,7 +639,7 @@ bool prefer_big_tiles(int64_t big_tiles, int64_t small_tiles) {
   return big_load < small_load * TileSet<T>::kBigRate;
 }
 
-template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false>
+template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false>
 int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
   g.tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
   g.tiles_n = (g.N + Cfg::BN - 1) / Cfg::BN;
@@ -611,7 +647,7 @@ int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, c
   if (tiles == 0 || batch == 0) return 0;
   PTO_REQUIRE(tiles < (1ll << 31) && batch < 65536, std::string(name) + ": grid too large");
   ProfScope ps(name, stream);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi, QN>), dim3((unsigned)tiles, (unsigned)batch),
+  hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi, QN, PT>), dim3((unsigned)tiles, (unsigned)batch),
                      dim3(Cfg::NT), 0, stream, g, epi);
   PTO_LAUNCHED(name);
   return 0;
@@ -653,22 +689,30 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
 // C[b](i,j) = sum_k P[b](i,k) * Q[b](k,j) with Q stored [K][N] (row pitch
 // ldq, N contiguous), bf16 only. Q must hold K rows of ldq elements, and
 // its rows past the true contraction length must be zero (as the pad
-// columns of P are).
-template <class Epi>
+// columns of P are). With PT, P is stored [K][M] as well (row pitch ldp,
+// ldp >= M, K rows, the rows past the true K zero) — for a symmetric P
+// that is P itself. UPPER (with PT): a symmetric product on upper tiles,
+// mirrored, as in launch_gemm.
+template <class Epi, bool PT = false, bool UPPER = false>
 int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
-  typedef typename TileSet<bf16>::big Big;
-  typedef typename TileSet<bf16>::small Small;
+  static_assert(PT || !UPPER, "symmetric QN products need PT");
+  typedef typename PickTiles<bf16, UPPER>::Big Big;
+  typedef typename PickTiles<bf16, UPPER>::Small Small;
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
+  PTO_REQUIRE(!UPPER || g.M == g.N, std::string(name) + ": symmetric product needs M == N");
   PTO_REQUIRE(g.K % (kStages * Big::BK) == 0 && g.K % (kStages * Small::BK) == 0, std::string(name) + ": K not padded");
-  PTO_REQUIRE(g.ldq < (int64_t(1) << 26), std::string(name) + ": row pitch too large");  // 64-byte K steps in 32 bits
-  PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 &&
+  PTO_REQUIRE(g.ldq < (int64_t(1) << 26) && g.ldp < (int64_t(1) << 26),
+              std::string(name) + ": row pitch too large");  // 64-byte K steps in 32 bits
+  PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 && (!PT || (g.ldp >= g.M && g.ldp >= 8)) &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
-  const int64_t big_tiles = (int64_t)((g.M + Big::BM - 1) / Big::BM) * ((g.N + Big::BN - 1) / Big::BN) * batch;
-  const int64_t small_tiles = (int64_t)((g.M + Small::BM - 1) / Small::BM) * ((g.N + Small::BN - 1) / Small::BN) * batch;
+  const int64_t tm = (g.M + Big::BM - 1) / Big::BM, tn = (g.N + Big::BN - 1) / Big::BN;
+  const int64_t sm = (g.M + Small::BM - 1) / Small::BM, sn = (g.N + Small::BN - 1) / Small::BN;
+  const int64_t big_tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
+  const int64_t small_tiles = (UPPER ? sm * (sm + 1) / 2 : sm * sn) * batch;
   if (prefer_big_tiles<bf16, Big, Small>(big_tiles, small_tiles))
-    return launch_gemm_cfg<bf16, Big, false, Epi, true>(g, epi, batch, stream, name);
-  return launch_gemm_cfg<bf16, Small, false, Epi, true>(g, epi, batch, stream, name);
+    return launch_gemm_cfg<bf16, Big, UPPER, Epi, true, PT>(g, epi, batch, stream, name);
+  return launch_gemm_cfg<bf16, Small, UPPER, Epi, true, PT>(g, epi, batch, stream, name);
 }
 
 // ------------------------------------------------------------- epilogues

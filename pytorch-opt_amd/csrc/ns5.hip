@@ -120,8 +120,8 @@ size_t ns5_ws_bytes_t(int64_t batch, int64_t rows, int64_t cols) {
   typedef typename AccOf<T>::type A;
   add(sizeof(double) * kRedBlocks * batch);   // partial sums
   add(sizeof(A) * batch);                      // scales
-  add(e * batch * m * ldm);                    // A
-  add(e * batch * m * ldm);                    // B
+  add(e * batch * ldm * ldm);                  // A (ldm rows: pad rows for the transposed read)
+  add(e * batch * ldm * ldm);                  // B'
   if (ns5_qn<T>()) {
     add(e * batch * ldm * ldn);                // X ping
     add(e * batch * ldm * ldn);                // X pong
@@ -147,8 +147,11 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
   Carver cv(ws, ws_bytes);
   double* partial = cv.take<double>(kRedBlocks * batch);
   A* scale = cv.take<A>(batch);
-  T* Ab = cv.take<T>(batch * m * ldm);
-  T* Bb = cv.take<T>(batch * m * ldm);
+  // A and B' hold ldm rows so that the bf16 update can read the symmetric
+  // B' as its own transpose ([K][M], K = ldm, pad rows zero)
+  const int64_t sAB = ldm * ldm;
+  T* Ab = cv.take<T>(batch * sAB);
+  T* Bb = cv.take<T>(batch * sAB);
   const int64_t sX = QN ? ldm * ldn : m * ldn;  // batch stride of X
   T* X[2];
   T* XT[2] = {nullptr, nullptr};
@@ -197,8 +200,10 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
     }
     if (launch_zero_cols<T>(XT[1], n, ldm, m, n * ldm, nb, stream)) return -1;
   }
-  if (launch_zero_cols<T>(Ab, m, ldm, m, m * ldm, nb, stream)) return -1;
-  if (launch_zero_cols<T>(Bb, m, ldm, m, m * ldm, nb, stream)) return -1;
+  if (launch_zero_cols<T>(Ab, m, ldm, m, sAB, nb, stream)) return -1;
+  if (launch_zero_cols<T>(Bb, m, ldm, m, sAB, nb, stream)) return -1;
+  if (launch_zero_cols<T>(Ab + m * ldm, ldm - m, ldm, 0, sAB, nb, stream)) return -1;  // pad rows
+  if (launch_zero_cols<T>(Bb + m * ldm, ldm - m, ldm, 0, sAB, nb, stream)) return -1;
 
   int cur = 0;  // X[cur] (QN) or XT[cur] holds the current iterate
   for (int64_t t = 0; t < steps; ++t) {
@@ -207,15 +212,19 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
     // 1. A = X·Xᵀ
     {
       GemmArgs g{Xc, ldn, sX, Xc, ldn, sX, (int)m, (int)m, (int)ldn, 0, 0, nullptr};
-      EpiStore<T, A> e{Ab, ldm, m * ldm, vec_ok<T>(Ab, ldm, m * ldm)};
+      EpiStore<T, A> e{Ab, ldm, sAB, vec_ok<T>(Ab, ldm, sAB)};
       if (launch_gemm<T, true>(g, e, nb, stream, "ns5_gram")) return -1;
     }
     // 2. B' = a·I + b·A + c·A·A
     {
-      GemmArgs g{Ab, ldm, m * ldm, Ab, ldm, m * ldm, (int)m, (int)m, (int)ldm, 0, 0, nullptr};
-      EpiNsSq<T, A> e{Ab, Bb, ldm, m * ldm, static_cast<A>(a), static_cast<A>(b), static_cast<A>(c),
-                      vec_ok<T>(Ab, ldm, m * ldm) && vec_ok<T>(Bb, ldm, m * ldm)};
-      if (launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
+      GemmArgs g{Ab, ldm, sAB, Ab, ldm, sAB, (int)m, (int)m, (int)ldm, 0, 0, nullptr};
+      EpiNsSq<T, A> e{Ab, Bb, ldm, sAB, static_cast<A>(a), static_cast<A>(b), static_cast<A>(c),
+                      vec_ok<T>(Ab, ldm, sAB) && vec_ok<T>(Bb, ldm, sAB)};
+      if constexpr (QN) {  // A is symmetric: both operands read as its own transpose
+        if (launch_gemm_qn<EpiNsSq<T, A>, true, true>(g, e, nb, stream, "ns5_square")) return -1;
+      } else {
+        if (launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
+      }
     }
     // 3. X' = B'·X   (QN: over X itself; else as B'·(Xᵀ)ᵀ over the stored
     //    transpose, X written in place since this product does not read it)
@@ -237,10 +246,11 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
       e.vec_d = e.dst && vec_ok<T>(e.dst, e.ld_d, e.s_d);
       e.vec_t = e.dstT && vec_ok<T>(e.dstT, e.ld_t, e.s_t);
       if constexpr (QN) {
-        GemmArgs g{Bb, ldm, m * ldm, Xc, ldn, sX, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
-        if (launch_gemm_qn(g, e, nb, stream, "ns5_update")) return -1;
+        // B' is symmetric: read as its own transpose (PT), like X (QN)
+        GemmArgs g{Bb, ldm, sAB, Xc, ldn, sX, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
+        if (launch_gemm_qn<EpiNsUpdate<T, A>, true>(g, e, nb, stream, "ns5_update")) return -1;
       } else {
-        GemmArgs g{Bb, ldm, m * ldm, XT[cur], ldm, n * ldm, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
+        GemmArgs g{Bb, ldm, sAB, XT[cur], ldm, n * ldm, (int)m, (int)n, (int)ldm, 0, 0, nullptr};
         if (launch_gemm<T, false>(g, e, nb, stream, "ns5_update")) return -1;
       }
     }
