@@ -435,3 +435,55 @@ def test_adamw_bf16_follows_torch_rounding(native_backend):
         ulp = b.float().abs() * 2.0 ** -7 + 1e-30
         assert float((diff <= ulp).float().mean()) >= 0.999
         assert float((diff == 0).float().mean()) >= 0.95
+
+
+# ---------------------------------------------------------------- SOAP / K-FAC at size
+
+def test_soap_step_at_size_vs_oracle(native_backend):
+    """One SOAP step of a 512x768 fp32 matrix from a refreshed state with
+    full-rank factors: rotations, Adam-in-basis and the update vs the numpy
+    oracle started from the same state (no refresh in the checked step)."""
+    from oracle import optim_oracle as oopt
+    from pytorch_opt import SOAP
+
+    torch.manual_seed(41)
+    p = torch.nn.Parameter(0.1 * torch.randn(512, 768, device=DEV))
+    kw = dict(lr=1e-2, betas=(0.9, 0.95), shampoo_beta=0.9, precondition_frequency=5)
+    opt = SOAP([p], max_preconditioner_dim=1024, **kw)
+    for _ in range(3):  # factors reach full rank; refresh at step 0 only
+        p.grad = torch.randn(512, 768, device=DEV)
+        opt.step()
+    g = torch.randn(512, 768, device=DEV)
+    p.grad = g
+    st = {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in opt.state[p].items() if k != "stale"}
+    want_p, _ = oopt.soap_matrix_step(p.detach().cpu().numpy(), g.cpu().numpy(), st, **kw)
+    opt.step()
+    assert np.abs(p.detach().cpu().numpy() - want_p).max() < 5e-5
+
+
+def test_kfac_direction_at_size_vs_oracle(native_backend):
+    """K-FAC natural gradient of a 1024x(768+1) fp32 layer (factors from 4096
+    tokens) vs the float64 closed form; EKFAC's first direction vs its oracle."""
+    from oracle import optim_oracle as oopt
+    from pytorch_opt import EKFAC, KFAC
+
+    torch.manual_seed(42)
+    model = torch.nn.Sequential(torch.nn.Linear(768, 1024)).to(DEV)
+    X = torch.randn(4096, 768, device=DEV)
+    for cls in (KFAC, EKFAC):
+        opt = cls(model, lr=1.0, momentum=0.0, damping=1e-3)
+        model.zero_grad()
+        (0.5 * torch.tanh(model(X)).pow(2).sum() / 4096).backward()
+        V = torch.cat([model[0].weight.grad, model[0].bias.grad.unsqueeze(1)], 1)
+        opt._refresh_inverses()
+        got = opt._precondition("0", V).double().cpu().numpy()
+        f = opt.tracker.factors["0"]
+        if cls is KFAC:
+            want = oopt.kfac_direction(V.double().cpu().numpy(), f["A"].double().cpu().numpy(),
+                                       f["G"].double().cpu().numpy(), 1e-3)
+        else:
+            inv = opt._inv["0"]
+            want, _ = oopt.ekfac_direction(V.double().cpu().numpy(), inv["QA"].double().cpu().numpy(),
+                                           inv["QG"].double().cpu().numpy(), None, 0.95, 1e-3)
+        assert _relfro(got, want) < 1e-3, cls.__name__
+        opt.tracker.remove()
