@@ -88,6 +88,17 @@ def test_ns5_bf16_vs_oracle(native_backend, shape):
     assert _relfro(_np(got), want) <= 2e-2
 
 
+@pytest.mark.parametrize("coeffs", [(1.5, -0.5, 0.0), (3.0, -3.2, 1.2), (2.0, 0.0, -0.25)])
+def test_ns5_bf16_coefficient_forms(native_backend, coeffs):
+    """bf16 batches with other coefficient sets: cubic Newton–Schulz (c = 0),
+    a general quintic, and b = 0."""
+    G = (torch.randn(3, 200, 520) * 1e-3).bfloat16()
+    got = ops.newton_schulz_orthogonalize(G.to(DEV), steps=5, coeffs=coeffs)
+    for i in range(3):
+        want = oo.ns5(G[i].float().numpy(), steps=5, coeffs=coeffs)
+        assert _relfro(_np(got[i]), want) <= 2e-2, (coeffs, i)
+
+
 def test_ns5_semi_orthogonal_bf16(native_backend):
     Q, _ = torch.linalg.qr(torch.randn(512, 256, dtype=torch.float64))
     Q = Q.T.contiguous()  # 256 x 512, rows orthonormal
