@@ -139,6 +139,69 @@ __global__ void __launch_bounds__(256) pack_kernel_f64(const TI* __restrict__ in
   }
 }
 
+// pack_kernel for 2- and 4-byte element types with 16-byte global accesses:
+// each thread reads runs of VEC = 16 / sizeof elements along an input row,
+// writes the straight copy from registers and the transposed copy through
+// an LDS tile held transposed (tt[c][r], rows padded by VEC elements so
+// that every tile row starts 16-byte aligned). Same values and padding as
+// pack_kernel. Needs 16-byte aligned bases and pitches and batch strides
+// that are multiples of VEC.
+template <typename TI, typename TO, typename S>
+__global__ void __launch_bounds__(256) pack_vec_kernel(const TI* __restrict__ in, int64_t rows, int64_t cols,
+                                                       int64_t ld_in, int64_t s_in, const S* __restrict__ scale,
+                                                       TO* __restrict__ out_s, int64_t ld_s, int64_t s_s,
+                                                       TO* __restrict__ out_t, int64_t ld_t, int64_t s_t, int ones) {
+  static_assert(sizeof(TI) == sizeof(TO) && (sizeof(TI) == 2 || sizeof(TI) == 4), "2- or 4-byte types");
+  constexpr int VEC = 16 / (int)sizeof(TI);
+  constexpr int CPR = 64 / VEC;  // 16-byte runs per 64-element tile row
+  constexpr int P = 64 + VEC;    // LDS pitch in elements
+  __shared__ __attribute__((aligned(16))) TO tt[64 * P];
+  const int b = blockIdx.z;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const TI* ib = in + (int64_t)b * s_in;
+  const S sc = scale ? scale[b] : S(1);
+  for (int q = threadIdx.x; q < 64 * CPR; q += 256) {
+    const int rr = q / CPR, cc = (q % CPR) * VEC;
+    const int64_t r = r0 + rr, c = c0 + cc;
+    TO v[VEC];
+    if (r < rows && c + VEC <= cols) {
+      const uint4 u = *reinterpret_cast<const uint4*>(ib + r * ld_in + c);
+      const TI* e = reinterpret_cast<const TI*>(&u);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) v[k] = static_cast<TO>(static_cast<float>(static_cast<S>(to_f(e[k])) * sc));
+    } else {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        float x = 0.f;
+        if (r < rows && c + k < cols) x = static_cast<float>(static_cast<S>(to_f(ib[r * ld_in + c + k])) * sc);
+        else if (ones && r < rows && c + k == cols) x = 1.f;
+        v[k] = static_cast<TO>(x);
+      }
+    }
+    if (out_s && r < rows && c < ld_s) {  // the ones column is not part of the straight copy
+      uint4 u;
+      TO* w = reinterpret_cast<TO*>(&u);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) w[k] = c + k < cols ? v[k] : static_cast<TO>(0.f);
+      *reinterpret_cast<uint4*>(out_s + (int64_t)b * s_s + r * ld_s + c) = u;
+    }
+    if (out_t) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) tt[(cc + k) * P + rr] = v[k];
+    }
+  }
+  if (!out_t) return;
+  __syncthreads();
+  TO* ob = out_t + (int64_t)b * s_t;
+  const int64_t trows = cols + (ones ? 1 : 0);
+  for (int q = threadIdx.x; q < 64 * CPR; q += 256) {
+    const int cc = q / CPR, rr = (q % CPR) * VEC;  // output row c0 + cc, columns r0 + rr ..
+    const int64_t c = c0 + cc, r = r0 + rr;
+    if (c < trows && r < ld_t)
+      *reinterpret_cast<uint4*>(ob + c * ld_t + r) = *reinterpret_cast<const uint4*>(&tt[cc * P + rr]);
+  }
+}
+
 // Straight copy only (no transposed output, no ones column): rows of 16-byte
 // runs, out(r, c) = s_b * in(r, c) for c < cols and 0 for cols <= c < ld_out.
 // Same value conversion as pack_kernel. Needs 16-byte aligned bases and
@@ -204,6 +267,19 @@ int launch_pack(const TI* in, int64_t rows, int64_t cols, int64_t ld_in, int64_t
   if (out_t) rext = std::max<int64_t>(rext, ld_t);
   dim3 grid((unsigned)((cext + 63) / 64), (unsigned)((rext + 63) / 64), (unsigned)batch);
   PTO_REQUIRE(grid.y < 65536 && grid.z < 65536, "pack: grid too large");
+  if constexpr (sizeof(TI) == sizeof(TO) && (sizeof(TI) == 2 || sizeof(TI) == 4) && sizeof(S) == 4) {
+    constexpr int VEC = 16 / (int)sizeof(TI);
+    auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    const bool vec = al(in) && ld_in % VEC == 0 && s_in % VEC == 0 &&
+                     (!out_s || (al(out_s) && ld_s % VEC == 0 && s_s % VEC == 0)) &&
+                     (!out_t || (al(out_t) && ld_t % VEC == 0 && s_t % VEC == 0));
+    if (vec) {
+      hipLaunchKernelGGL((pack_vec_kernel<TI, TO, S>), grid, dim3(256), 0, stream, in, rows, cols, ld_in, s_in,
+                         scale, out_s, ld_s, s_s, out_t, ld_t, s_t, ones ? 1 : 0);
+      PTO_LAUNCHED("pack_vec");
+      return 0;
+    }
+  }
   if (sizeof(S) == 8 || sizeof(TO) == 8 || sizeof(TI) == 8)
     hipLaunchKernelGGL((pack_kernel_f64<TI, TO, S>), grid, dim3(256), 0, stream, in, rows, cols, ld_in, s_in, scale,
                        out_s, ld_s, s_s, out_t, ld_t, s_t, ones ? 1 : 0);
