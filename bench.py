@@ -343,9 +343,11 @@ KFAC_D, KFAC_DEPTH, KFAC_TOKENS = 2048, 4, 8192
 
 
 def bench_kfac(torch, dev, cpu):
-    """K-FAC and EKFAC optimizer steps on 4 x Linear(2048, 2048) with bias,
-    8192 tokens, fp32, over one inv_every = 10 period: step 0 refreshes the
-    8 damped inverses / eigenbases (float64 eigh of 2049² and 2048², batched),
+    """K-FAC (eigh and Newton inverses) and EKFAC optimizer steps on
+    4 x Linear(2048, 2048) with bias, 8192 tokens, fp32, over one inv_every =
+    10 period after an untimed one: step 0 refreshes the 8 damped inverses /
+    eigenbases (float64 eigh of 2049² and 2048², batched, or the batched
+    coupled Newton iteration in fp32 with inverse_method="newton"),
     steps 1-9 only precondition (two MFMA products per layer) and update.
     The backward-hook factor statistics are outside opt.step() and are timed
     by the K-FAC Gram line of `factors`."""
@@ -354,13 +356,14 @@ def bench_kfac(torch, dev, cpu):
     d, depth, tokens = KFAC_D, KFAC_DEPTH, KFAC_TOKENS
     flops = depth * (2 * d * d * (d + 1) + 2 * d * (d + 1) * (d + 1))  # iG·V, (iG·V)·iA per layer
     out = {"workload": f"{depth} x Linear({d}, {d}) + bias, {tokens} tokens, fp32, inv_every 10"}
-    for name, cls in (("kfac", KFAC), ("ekfac", EKFAC)):
+    arms = (("kfac", KFAC, {}), ("kfac_newton", KFAC, {"inverse_method": "newton"}), ("ekfac", EKFAC, {}))
+    for name, cls, kw in arms:
         torch.manual_seed(7)
         model = torch.nn.Sequential(*[torch.nn.Linear(d, d) for _ in range(depth)]).to(dev)
-        opt = cls(model, lr=1e-3, damping=1e-3, inv_every=10)
+        opt = cls(model, lr=1e-3, damping=1e-3, inv_every=10, **kw)
         X = torch.randn(tokens, d, device=dev)
         per = []
-        for _ in range(10):
+        for _ in range(20):  # one untimed period, then one timed period starting with a refresh
             opt.zero_grad(set_to_none=True)
             (0.5 * model(X).pow(2).sum() / tokens).backward()
             torch.cuda.synchronize()
@@ -368,11 +371,14 @@ def bench_kfac(torch, dev, cpu):
             opt.step()
             torch.cuda.synchronize()
             per.append(time.perf_counter() - t0)
+        per = per[10:]
         plain = sum(per[1:]) / 9
         out[name] = {"refresh_step_ms": round(per[0] * 1e3, 1), "plain_step_ms": round(plain * 1e3, 2),
                      "mean_step_ms": round(sum(per) / 10 * 1e3, 2)}
         if name == "kfac":
             out[name]["plain_alg_tflops"] = round(flops / plain / 1e12, 2)
+        if name == "kfac_newton":
+            out[name]["inverse_method"] = "newton (coupled Newton, p = 1, fp32, batched)"
         del model, opt, X
         torch.cuda.empty_cache()
     if cpu:
@@ -394,6 +400,7 @@ def bench_kfac(torch, dev, cpu):
                       "sample": "numpy oracle: one (G·V)·A product of 2048x2049 and one float64 eigh of 2049², "
                                 "scaled by 4 layers (and 8 eighs per refresh); mean over one 10-step period"}
         out["kfac_speedup_vs_cpu"] = round(out["cpu"]["kfac_mean_step_ms"] / out["kfac"]["mean_step_ms"], 1)
+        out["kfac_newton_speedup_vs_cpu"] = round(out["cpu"]["kfac_mean_step_ms"] / out["kfac_newton"]["mean_step_ms"], 1)
     return out
 
 

@@ -22,6 +22,8 @@ from .kfac import KFAC, batched_eigh
 
 class EKFAC(KFAC):
     def __init__(self, model, *args, scale_decay: float = 0.95, **kwargs):
+        if kwargs.get("inverse_method", "eigh") != "eigh":
+            raise ValueError("EKFAC preconditions in the factors' eigenbases: inverse_method must be 'eigh'")
         self._scales: dict[str, torch.Tensor] = {}
         self._scale_decay = scale_decay
         super().__init__(model, *args, **kwargs)

@@ -15,6 +15,11 @@ then optional global norm clipping, momentum, weight decay and the step
 Here the factor statistics are ops.gram_update_ calls (through KronTracker),
 the preconditioning is ops.precond_apply_two_sided — both MFMA kernels on a
 GPU — and the refresh eighs of same-shape factors run as one batched call.
+``inverse_method="newton"`` (an addition; the default "eigh" is the
+reference's) computes the damped inverses instead with the coupled Newton
+iteration of ops.inverse_matrix_root at p = 1 — the MFMA root kernels — on
+the same batches, in the factors' precision, with the condition numbers of
+the diagnostics estimated by power iteration.
 """
 
 from __future__ import annotations
@@ -29,6 +34,46 @@ from ..curvature.kron import KronTracker
 from ._common import DiagnosticsMixin, StepTimer, adamw_update, validate_checkpoint_groups, validate_groups
 
 _FISHER_MODES = ("empirical", "sampled")
+_INVERSE_METHODS = ("eigh", "newton")
+
+
+def _top_eigenvalues(M: torch.Tensor, iters: int) -> torch.Tensor:
+    """Largest eigenvalue of each symmetric PSD matrix of a batch, by power
+    iteration from a fixed start (a lower estimate after few steps)."""
+    g = torch.Generator(device=M.device).manual_seed(0)
+    v = torch.randn(M.shape[0], M.shape[-1], 1, generator=g, device=M.device, dtype=M.dtype)
+    for _ in range(iters):
+        v = M @ v
+        v = v / v.norm(dim=1, keepdim=True).clamp_min(torch.finfo(M.dtype).tiny)
+    return (v.mT @ (M @ v)).reshape(-1)
+
+
+def damped_inverses_newton(mats, gammas, batch_bytes: int = 4 << 30, power_iters: int = 30):
+    """(F_i + γ_i·I)⁻¹ for each factor by the coupled Newton iteration of
+    ops.inverse_matrix_root with p = 1 (the MFMA root kernels on a GPU),
+    same-shape factors in one batched call, in the factor's precision
+    (float64 factors in float64, others in float32). Also returns the
+    condition number of each F_i + γ_i·I estimated as λ_max(F + γI)·λ_max
+    of the inverse, both by power iteration. Returns [(inverse, cond)]."""
+    out = [None] * len(mats)
+    buckets = {}
+    for i, F in enumerate(mats):
+        buckets.setdefault((tuple(F.shape), F.device, F.dtype), []).append(i)
+    for (shape, dev, dt), idx in buckets.items():
+        n = shape[-1]
+        rdt = torch.float64 if dt == torch.float64 else torch.float32
+        # the root's own workspace holds several n x n matrices per entry
+        step = max(1, batch_bytes // (8 * n * n * torch.finfo(rdt).bits // 8))
+        eye = torch.eye(n, device=dev, dtype=rdt)
+        for s in range(0, len(idx), step):
+            chunk = idx[s:s + step]
+            M = torch.stack([mats[i].to(rdt) + gammas[i] * eye for i in chunk])
+            inv = ops.inverse_matrix_root(M, 1, damping=0.0, method="newton", root_dtype=rdt,
+                                          tol=1e-10 if rdt == torch.float64 else 1e-5)
+            cond = (_top_eigenvalues(M, power_iters) * _top_eigenvalues(inv, power_iters)).tolist()
+            for j, i in enumerate(chunk):
+                out[i] = (inv[j].to(dt), cond[j])
+    return out
 
 
 def batched_eigh(mats, batch_bytes: int = 4 << 30):
@@ -53,11 +98,14 @@ class KFAC(Optimizer, DiagnosticsMixin):
                  ema_decay: float | None = 0.95, momentum: float = 0.9, stats_every: int = 1, inv_every: int = 10,
                  fisher_mode: str = "empirical", weight_decay: float = 0.0, max_grad_norm: float | None = None, *,
                  params=None, adamw_lr: float = 3e-4, adamw_betas: tuple = (0.9, 0.95), adamw_eps: float = 1e-8,
-                 adamw_wd: float = 0.0):
+                 adamw_wd: float = 0.0, inverse_method: str = "eigh"):
         if fisher_mode not in _FISHER_MODES:
             raise ValueError(f"fisher_mode must be one of {_FISHER_MODES}, got {fisher_mode!r}")
         if stats_every < 1 or inv_every < 1:
             raise ValueError("stats_every and inv_every must be positive")
+        if inverse_method not in _INVERSE_METHODS:
+            raise ValueError(f"inverse_method must be one of {_INVERSE_METHODS}, got {inverse_method!r}")
+        self.inverse_method = inverse_method
         self.model = model
         self.fisher_mode = fisher_mode
         owners = {}
@@ -159,12 +207,20 @@ class KFAC(Optimizer, DiagnosticsMixin):
         g = self.param_groups[0]
         names = list(self.tracker.factors)
         facs = [self.tracker.factors[n] for n in names]
-        eig = batched_eigh([F for f in facs for F in (f["A"], f["G"])])
+        gammas = [kfac_factored_damping(f["A"], f["G"], g["damping"]) for f in facs]
+        if self.inverse_method == "newton":
+            res = damped_inverses_newton([F for f in facs for F in (f["A"], f["G"])],
+                                         [gm for pair in gammas for gm in pair])
+        else:
+            eig = batched_eigh([F for f in facs for F in (f["A"], f["G"])])
         conds = []
         for i, (name, f) in enumerate(zip(names, facs)):
-            gamma_A, gamma_G = kfac_factored_damping(f["A"], f["G"], g["damping"])
-            iA, cA = self._damped_inverse_from(*eig[2 * i], gamma_A, f["A"].dtype)
-            iG, cG = self._damped_inverse_from(*eig[2 * i + 1], gamma_G, f["G"].dtype)
+            gamma_A, gamma_G = gammas[i]
+            if self.inverse_method == "newton":
+                (iA, cA), (iG, cG) = res[2 * i], res[2 * i + 1]
+            else:
+                iA, cA = self._damped_inverse_from(*eig[2 * i], gamma_A, f["A"].dtype)
+                iG, cG = self._damped_inverse_from(*eig[2 * i + 1], gamma_G, f["G"].dtype)
             self._inv[name] = {"iA": iA, "iG": iG, "cond_A": cA, "cond_G": cG}
             conds.append((cA, cG))
         return conds

@@ -474,15 +474,16 @@ def test_soap_step_at_size_vs_oracle(native_backend):
 
 def test_kfac_direction_at_size_vs_oracle(native_backend):
     """K-FAC natural gradient of a 1024x(768+1) fp32 layer (factors from 4096
-    tokens) vs the float64 closed form; EKFAC's first direction vs its oracle."""
+    tokens; eigh and Newton inverses) vs the float64 closed form; EKFAC's
+    first direction vs its oracle."""
     from oracle import optim_oracle as oopt
     from pytorch_opt import EKFAC, KFAC
 
     torch.manual_seed(42)
     model = torch.nn.Sequential(torch.nn.Linear(768, 1024)).to(DEV)
     X = torch.randn(4096, 768, device=DEV)
-    for cls in (KFAC, EKFAC):
-        opt = cls(model, lr=1.0, momentum=0.0, damping=1e-3)
+    for cls, kw in ((KFAC, {}), (KFAC, {"inverse_method": "newton"}), (EKFAC, {})):
+        opt = cls(model, lr=1.0, momentum=0.0, damping=1e-3, **kw)
         model.zero_grad()
         (0.5 * torch.tanh(model(X)).pow(2).sum() / 4096).backward()
         V = torch.cat([model[0].weight.grad, model[0].bias.grad.unsqueeze(1)], 1)
@@ -496,5 +497,5 @@ def test_kfac_direction_at_size_vs_oracle(native_backend):
             inv = opt._inv["0"]
             want, _ = oopt.ekfac_direction(V.double().cpu().numpy(), inv["QA"].double().cpu().numpy(),
                                            inv["QG"].double().cpu().numpy(), None, 0.95, 1e-3)
-        assert _relfro(got, want) < 1e-3, cls.__name__
+        assert _relfro(got, want) < 1e-3, (cls.__name__, kw)
         opt.tracker.remove()
