@@ -11,15 +11,14 @@
 //   return sym(X) in the input dtype
 // `err` is one maximum over the whole batch, as in the reference.
 //
-// Symmetric formulation. In exact arithmetic Mk, Mi and every power of Mi
-// are symmetric (all are polynomials in M). Here they are symmetric by
-// construction: Mi^p and Mi^p·Mk are computed on upper tiles only and
-// mirrored. That halves the MFMA work of three of the four products and is
-// also what keeps fp32 stable: with full products (the reference's form)
-// but symmetrised powers, Mk's antisymmetric rounding part is never
-// corrected and X drifts; with Mk kept symmetric the iteration converges
-// like the reference's (same err floor) with a smaller final residual.
-// X·Mi stays a full product (X is not symmetrised until the end).
+// Symmetric formulation. In exact arithmetic X, Mk, Mi and every power of
+// Mi are symmetric (all are polynomials in M). Here Mi^p and Mi^p·Mk (and
+// in fp64 also X·Mi) are symmetric by construction: computed on upper
+// tiles only and mirrored. That halves their MFMA work and is also what
+// keeps fp32 stable: with full products (the reference's form) but
+// symmetrised powers, Mk's antisymmetric rounding part is never corrected
+// and X drifts; with Mk kept symmetric the iteration converges like the
+// reference's (same err floor) with a smaller final residual.
 //
 // Device-side control: every kernel of an iteration checks a device flag
 // and exits at once after the stop decision, and a one-thread kernel makes
@@ -298,10 +297,14 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     return launch_gemm<R, false>(g, e, nb, stream, name);
   };
 
+  // X·Mi on upper tiles in fp64 only: in fp32 the full product, averaged by
+  // the final symmetrisation, ends the non-converging ill-conditioned runs
+  // (cond ~1e6) on a ~15% lower residual.
+  constexpr bool kSymX = sizeof(R) == 8;
   auto iteration = [&](int it) -> int {
     const int cur = it & 1, nxt = cur ^ 1;
-    // X_{it+1} = X_it · Mi
-    if (product(X[cur], Mi[cur], X[nxt], false, "root_xmi")) return -1;
+    // X_{it+1} = X_it · Mi (symmetric: both are polynomials in M)
+    if (product(X[cur], Mi[cur], X[nxt], kSymX, "root_xmi")) return -1;
     // S = Mi^p (torch.linalg.matrix_power order: direct for p <= 3, else
     // binary powering from the least significant bit)
     const R* S = nullptr;
