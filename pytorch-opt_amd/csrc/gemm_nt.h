@@ -205,13 +205,14 @@ struct LdsPlan {
   static constexpr int WPA = (NW + kStages - 1) / kStages;  // waves per array in the epilogue
   static constexpr int SP = WTN + 1;
   static constexpr int kLdsMax = 160 * 1024;
-  // rows per epilogue pass: at most 64, halved until the four arrays fit
+  // rows per epilogue pass: the largest multiple of 16, at most 64, that
+  // divides the wave tile's rows and lets the four arrays fit
   static constexpr int pick_rpp() {
-    int r = WTM < 64 ? WTM : 64;
-    while (r > 16 && kStages * (STAGE > WPA * r * SP * (int)sizeof(S) ? STAGE : WPA * r * SP * (int)sizeof(S)) >
-                         kLdsMax)
-      r /= 2;
-    return r;
+    for (int r = (WTM < 64 ? WTM : 64) / 16 * 16; r > 16; r -= 16) {
+      const int epi = WPA * r * SP * (int)sizeof(S);
+      if (WTM % r == 0 && kStages * (STAGE > epi ? STAGE : epi) <= kLdsMax) return r;
+    }
+    return 16;
   }
   static constexpr int RPP = pick_rpp();
   static constexpr int EPI = WPA * RPP * SP * (int)sizeof(S);
@@ -494,6 +495,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   constexpr int RPB = 64 / LGD;
   constexpr int CBLK = RUNS / LGD;
   constexpr int ITEMS = ((RPP + RPB - 1) / RPB) * CBLK;  // direct runs per lane
+  // when LGD does not divide 64 (wave tiles 48 wide) the last 64 % LGD lanes
+  // would repeat the next block's first runs: they sit out
+  const bool lane_ok = LGD * RPB == 64 || lane < LGD * RPB;
   // transposed runs: 8 lanes share a column c and cover 64 consecutive rows
   constexpr int CBT = WTN / 8;
   constexpr int ITEMS_T = ((RPP / 8 + 7) / 8) * CBT;
@@ -510,7 +514,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       const int i = pr0 + r, j0 = wc0 + c;
       const int n = min(8, nrem - c);
       const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
-      if (r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);
+      if (lane_ok && r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);
     }
 #pragma unroll
     for (int fm = hp * (RPP / MF::MN); fm < (hp + 1) * (RPP / MF::MN); ++fm)
@@ -531,7 +535,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       const int i = pr0 + r, j0 = wc0 + c;
       const int n = min(8, nrem - c);
       const int kbeg = diag ? max(0, i - j0) : 0;
-      if (!(r < rows && c < nrem && kbeg < n)) continue;
+      if (!(lane_ok && r < rows && c < nrem && kbeg < n)) continue;
       S v[8], vo[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
@@ -584,7 +588,10 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 // need square tiles. kBigRate is the big tile's throughput per CU relative
 // to the small tile's (area per unit time, measured on MI355X over square
 // and rectangular products from 512 to 11008): the big tile reuses each
-// staged operand byte for more MFMA work.
+// staged operand byte for more MFMA work. bf16 symmetric products also
+// have a 192 x 192 "mid" tile (kMidRate, same units): a 4096² symmetric
+// product has 136 upper tiles of 256² for 256 CUs but 253 of 192², one
+// full round.
 template <typename T>
 struct TileSet;
 template <>
@@ -593,7 +600,10 @@ struct TileSet<bf16> {
   typedef Tile<128, 128, 32, 2, 2> small;
   typedef Tile<256, 256, 32, 2, 4> sym_big;
   typedef Tile<128, 128, 32, 2, 2> sym_small;
+  typedef Tile<192, 192, 32, 2, 4> sym_mid;
+  static constexpr bool kHasMid = true;
   static constexpr double kBigRate = 1.5;
+  static constexpr double kMidRate = 1.35;
 };
 template <>
 struct TileSet<float> {
@@ -601,7 +611,10 @@ struct TileSet<float> {
   typedef Tile<64, 64, 16, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
+  typedef big sym_mid;  // unused
+  static constexpr bool kHasMid = false;
   static constexpr double kBigRate = 1.22;
+  static constexpr double kMidRate = 0.0;
 };
 template <>
 struct TileSet<double> {
@@ -609,7 +622,10 @@ struct TileSet<double> {
   typedef Tile<32, 32, 8, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
+  typedef big sym_mid;  // unused
+  static constexpr bool kHasMid = false;
   static constexpr double kBigRate = 1.25;
+  static constexpr double kMidRate = 0.0;
 };
 
 // Compute units of the current device (256 on a full MI355X), cached per
@@ -664,6 +680,30 @@ struct PickTiles<T, true> {
   typedef typename TileSet<T>::sym_small Small;
 };
 
+// The same model over the big, small and (symmetric bf16) mid tiles of
+// launch_gemm: 0 = small, 1 = big, 2 = mid.
+template <typename T, bool UPPER>
+int pick_tile(int64_t M, int64_t N, int64_t batch) {
+  typedef typename PickTiles<T, UPPER>::Big Big;
+  typedef typename PickTiles<T, UPPER>::Small Small;
+  typedef typename TileSet<T>::sym_mid Mid;
+  const int64_t cus = device_cus();
+  auto load = [&](int bm, int bn, double rate) {
+    const int64_t tm = (M + bm - 1) / bm, tn = (N + bn - 1) / bn;
+    const int64_t tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
+    return double((tiles + cus - 1) / cus) * (bm * bn) / rate;
+  };
+  double best = load(Small::BM, Small::BN, 1.0);
+  int pick = 0;
+  const double big = load(Big::BM, Big::BN, TileSet<T>::kBigRate);
+  if (big < best) {
+    best = big;
+    pick = 1;
+  }
+  if (UPPER && TileSet<T>::kHasMid && load(Mid::BM, Mid::BN, TileSet<T>::kMidRate) < best) pick = 2;
+  return pick;
+}
+
 // Validate the operand contract and pick a tile size.
 template <typename T, bool UPPER, class Epi>
 int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
@@ -677,12 +717,13 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
-  const int64_t tm = (g.M + Big::BM - 1) / Big::BM, tn = (g.N + Big::BN - 1) / Big::BN;
-  const int64_t sm = (g.M + Small::BM - 1) / Small::BM, sn = (g.N + Small::BN - 1) / Small::BN;
-  const int64_t big_tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
-  const int64_t small_tiles = (UPPER ? sm * (sm + 1) / 2 : sm * sn) * batch;
-  if (prefer_big_tiles<T, Big, Small>(big_tiles, small_tiles))
-    return launch_gemm_cfg<T, Big, UPPER, Epi>(g, epi, batch, stream, name);
+  const int pick = pick_tile<T, UPPER>(g.M, g.N, batch);
+  if constexpr (UPPER && TileSet<T>::kHasMid) {
+    typedef typename TileSet<T>::sym_mid Mid;
+    static_assert(Mid::BM == Mid::BN && Mid::BK == Big::BK, "mid tile: square, same K tile");
+    if (pick == 2) return launch_gemm_cfg<T, Mid, UPPER, Epi>(g, epi, batch, stream, name);
+  }
+  if (pick == 1) return launch_gemm_cfg<T, Big, UPPER, Epi>(g, epi, batch, stream, name);
   return launch_gemm_cfg<T, Small, UPPER, Epi>(g, epi, batch, stream, name);
 }
 

@@ -138,6 +138,17 @@ def test_ns5_bf16_config2_full_size(native_backend, cols):
     assert _relfro(_np(got[0]), want0) <= 2e-2
 
 
+@pytest.mark.parametrize("cols", [4096, 11008])
+def test_ns5_bf16_single_matrix_full_size(native_backend, cols):
+    """One bf16 4096 x cols matrix, whose symmetric products (136 upper tiles
+    of 256²) run on 192² tiles, one round over the CUs: vs the package's
+    pure-torch fp32 reference on the GPU."""
+    G = _config2_inputs(1, 4096, cols, 3000)[0]
+    got = ops.newton_schulz_orthogonalize(G)
+    want = ops_ref.newton_schulz_orthogonalize(G.float())
+    assert float((got.float() - want).norm() / want.norm()) <= 2e-2
+
+
 # ---------------------------------------------------------------- kron
 
 @pytest.mark.parametrize("beta2", [1.0, 0.9, 0.95])
