@@ -494,6 +494,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   constexpr int LGD = RUNS < 8 ? RUNS : 8;
   constexpr int RPB = 64 / LGD;
   constexpr int CBLK = RUNS / LGD;
+  static_assert(RUNS % LGD == 0, "wave tile width: at most 64 columns or a multiple of 64");
   constexpr int ITEMS = ((RPP + RPB - 1) / RPB) * CBLK;  // direct runs per lane
   // when LGD does not divide 64 (wave tiles 48 wide) the last 64 % LGD lanes
   // would repeat the next block's first runs: they sit out
