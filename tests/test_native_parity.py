@@ -208,6 +208,38 @@ def test_gram_vs_oracle(native_backend, append_ones):
     assert _relfro(_np(F), want) <= 1e-6
 
 
+@pytest.mark.parametrize("d, append_ones", [(4000, True), (3900, False)])
+def test_gram_192_tile_ragged_vs_oracle(native_backend, d, append_ones):
+    """A single d ≈ 4000 factor takes the 192² symmetric tile (one round of
+    about 231 upper tiles); d + ones is not a tile multiple, so the last tile
+    row and column are partial, and the blend reads the prior there."""
+    g = torch.Generator().manual_seed(21)
+    X = torch.randn(512, d, generator=g).bfloat16()
+    dd = d + int(append_ones)
+    prior = torch.randn(dd, dd, generator=g)
+    prior = (prior + prior.T) / 2
+    F = prior.to(DEV)
+    ops.gram_update_(F, X.to(DEV), beta=0.9, alpha=0.1 / 512, append_ones=append_ones)
+    want = oo.gram_update(prior.numpy().astype(np.float64), X.double().numpy(), 0.9, 0.1 / 512, append_ones,
+                          dtype=np.float64)
+    assert _relfro(_np(F), want) <= 1e-6
+    assert torch.equal(F, F.T)
+
+
+def test_kron_bf16_192_tile(native_backend):
+    """bf16 factors of a 3000 x 200 gradient: L (3000²) on the 192² tile,
+    R (200²) on the small one; vs the float64 oracle at bf16 rounding."""
+    g = torch.Generator().manual_seed(22)
+    G = torch.randn(3000, 200, generator=g).bfloat16()
+    L = torch.zeros(3000, 3000, dtype=torch.bfloat16, device=DEV)
+    R = torch.zeros(200, 200, dtype=torch.bfloat16, device=DEV)
+    ops.kron_factor_update_(L, R, G.to(DEV), beta2=1.0)
+    Lo, Ro = oo.kron_factor_update(np.zeros((3000, 3000)), np.zeros((200, 200)), G.double().numpy(), 1.0,
+                                   dtype=np.float64)
+    assert _relfro(_np(L), Lo) <= 5e-3 and _relfro(_np(R), Ro) <= 5e-3
+    assert torch.equal(L, L.T)
+
+
 def test_gram_config3_full_size(native_backend):
     """bf16 A [16384, 4096] ~ N(0,1) -> fp32 AᵀA/16384 blended into a prior."""
     g = torch.Generator(device=DEV).manual_seed(3)
