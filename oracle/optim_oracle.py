@@ -12,7 +12,13 @@ Pinning (tests/test_oracle.py): adamw_step against torch.optim.Adam/AdamW;
 soap_matrix_step against the same Adam when the factors stay diagonal (the
 eigenbases are signed permutations, SOAP's analytic identity,
 tests/test_soap.py:8-24 of the reference) and against its own rotation-
-free form when Q_L, Q_R are fixed arbitrary orthogonal matrices.
+free form when Q_L, Q_R are fixed arbitrary orthogonal matrices;
+muon_matrix_step over two steps on gradients sharing singular vectors
+(Nesterov momentum, NS5 per singular value and the aspect-ratio lr factor
+in closed form); shampoo_matrix_step's first step on g = U·diag(s)·Vᵀ
+(P = U·diag(s·(s²+ε)^-½)·Vᵀ, with and without the AdaGrad graft);
+kfac_direction against the dense Kronecker solve; ekfac_direction with
+the factors' eigenvalue products as scales against kfac_direction.
 """
 
 from __future__ import annotations

@@ -334,3 +334,79 @@ def test_ekfac_direction_with_eigenvalue_scales_is_kfac():
     np.testing.assert_allclose(d, np.linalg.solve(G, V) @ np.linalg.inv(A), rtol=1e-9, atol=1e-12)
     d0, s0 = oopt.ekfac_direction(V, QA, QG, None, 0.9, 1e-3)
     np.testing.assert_allclose(s0, (QG.T @ V @ QA) ** 2, atol=1e-14)
+
+
+# ------------------------------------------------------- Muon / Shampoo steps
+
+def _svd_pair(m, n, rng):
+    """U (m x k), V (n x k), k = min(m, n), with orthonormal columns."""
+    k = min(m, n)
+    return _orth(m, rng)[:, :k], _orth(n, rng)[:, :k]
+
+
+@pytest.mark.parametrize("shape", [(8, 4), (4, 8)])
+def test_muon_oracle_step_closed_form(shape):
+    """Two Muon steps on gradients sharing singular vectors, g_t = U·diag(a_t)·Vᵀ:
+    Nesterov momentum gives u_2 = U·diag((1+μ)·a_2 + μ²·a_1)·Vᵀ, NS5 acts on its
+    singular values, and the spectral lr factor is max(1, rows/cols)^½. A
+    dropped μ² term, plain (non-Nesterov) momentum or an inverted aspect
+    ratio each fail."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(31)
+    m, n = shape
+    U, V = _svd_pair(m, n, rng)
+    k = min(m, n)
+    a1, a2 = rng.uniform(0.5, 2.0, k), rng.uniform(0.5, 2.0, k)
+    g1, g2 = (U * a1) @ V.T, (U * a2) @ V.T
+    mu, lr, wd = 0.9, 0.05, 0.1
+    p0 = rng.standard_normal((m, n))
+    p1, buf1, _ = oopt.muon_matrix_step(p0, g1, np.zeros((m, n)), lr=lr, momentum=mu, weight_decay=wd)
+    p2, buf2, O2 = oopt.muon_matrix_step(p1, g2, buf1, lr=lr, momentum=mu, weight_decay=wd)
+    want_O2 = _ns_closed_form(U, (1 + mu) * a2 + mu * mu * a1, V)
+    np.testing.assert_allclose(O2, want_O2, atol=2e-6)
+    np.testing.assert_allclose(buf2, (U * (mu * a1 + a2)) @ V.T, rtol=0, atol=1e-7)  # μ is cast to fp32
+    scale = max(1.0, m / n) ** 0.5
+    want_O1 = _ns_closed_form(U, (1 + mu) * a1, V)
+    want_p2 = (p0 * (1 - lr * wd) - lr * scale * want_O1) * (1 - lr * wd) - lr * scale * want_O2
+    np.testing.assert_allclose(p2, want_p2, atol=2e-6)
+    # planted slips move O2 or p2 by far more than the tolerance
+    assert np.abs(_ns_closed_form(U, (1 + mu) * a2 + mu * a1, V) - want_O2).max() > 1e-3
+    assert np.abs(_ns_closed_form(U, mu * a1 + a2, V) - want_O2).max() > 1e-3
+    if m != n:
+        wrong = max(1.0, n / m) ** 0.5
+        assert np.abs(lr * (wrong - scale) * want_O2).max() > 1e-3
+
+
+@pytest.mark.parametrize("shape", [(6, 9), (9, 6)])
+def test_shampoo_oracle_step_closed_form(shape):
+    """First Shampoo step (refresh at step 0) on g = U·diag(s)·Vᵀ with EMA
+    factors: L/bias = g·gᵀ and R/bias = gᵀ·g, so the roots are
+    U·diag((s²+ε)^-¼)·Uᵀ (plus ε^-¼ on the null space) and P = L_root·g·R_root
+    = U·diag(s·(s²+ε)^-½)·Vᵀ; without a graft p moves by lr·P. The AdaGrad
+    graft rescales P to ‖g/(√(g²)+δ)‖. A missing bias correction or a root
+    of the wrong order fails."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(32)
+    m, n = shape
+    U, V = _svd_pair(m, n, rng)
+    s = rng.uniform(0.5, 2.0, min(m, n))
+    g = (U * s) @ V.T
+    p0 = rng.standard_normal((m, n))
+    eps, lr, beta2 = 1e-6, 0.1, 0.9
+    zL, zR = np.zeros((m, m)), np.zeros((n, n))
+    out = oopt.shampoo_matrix_step(p0, g, zL, zR, None, None, np.zeros((m, n)), 0, 0, lr=lr, beta2=beta2,
+                                   eps=eps, graft="none")
+    P = (U * (s / np.sqrt(s * s + eps))) @ V.T
+    np.testing.assert_allclose(out[0], p0 - lr * P, atol=1e-6)
+    np.testing.assert_allclose(out[1], (1 - beta2) * g @ g.T, atol=1e-12)
+    # no bias correction: the roots see (1-β)·g·gᵀ and P grows by (1-β)^-½
+    P_nobias = (U * (s / np.sqrt((1 - beta2) * s * s + eps))) @ V.T
+    assert np.abs(P_nobias - P).max() > 1e-2
+    # inverse square roots instead of 4th roots change every singular value
+    assert np.abs((U * (s / (s * s + eps))) @ V.T - P).max() > 1e-2
+    out_g = oopt.shampoo_matrix_step(p0, g, zL, zR, None, None, np.zeros((m, n)), 0, 0, lr=lr, beta2=beta2,
+                                     eps=eps, graft="adagrad", diag_eps=1e-10)
+    target = np.linalg.norm(g / (np.abs(g) + 1e-10))
+    np.testing.assert_allclose(out_g[0], p0 - lr * P * (target / np.linalg.norm(P)), atol=1e-6)
