@@ -152,7 +152,8 @@ def test_ns5_bf16_single_matrix_full_size(native_backend, cols):
 # ---------------------------------------------------------------- kron
 
 @pytest.mark.parametrize("beta2", [1.0, 0.9, 0.95])
-@pytest.mark.parametrize("shape", [(4, 7), (64, 96), (300, 200), (129, 65)])
+@pytest.mark.parametrize("shape", [(4, 7), (64, 96), (300, 200), (129, 65),
+                                   (96, 96), (129, 129)])  # square G: both factors in one launch
 def test_kron_vs_oracle(native_backend, beta2, shape):
     m, n = shape
     g = torch.Generator().manual_seed(12)
@@ -166,8 +167,8 @@ def test_kron_vs_oracle(native_backend, beta2, shape):
     assert torch.equal(L, L.T) and torch.equal(R, R.T)
 
 
-def test_kron_nonsymmetric_prior_and_fp64(native_backend):
-    m, n = 70, 45
+@pytest.mark.parametrize("m, n", [(70, 45), (70, 70)])
+def test_kron_nonsymmetric_prior_and_fp64(native_backend, m, n):
     L0 = torch.randn(m, m, dtype=torch.float64)
     R0 = torch.randn(n, n, dtype=torch.float64)
     G = torch.randn(m, n, dtype=torch.float64)
