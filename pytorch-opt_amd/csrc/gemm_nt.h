@@ -617,10 +617,10 @@ struct TileSet<float> {
   typedef Tile<64, 64, 16, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
-  typedef big sym_mid;  // unused
-  static constexpr bool kHasMid = false;
+  typedef Tile<192, 192, 16, 2, 4> sym_mid;
+  static constexpr bool kHasMid = true;
   static constexpr double kBigRate = 1.22;
-  static constexpr double kMidRate = 0.0;
+  static constexpr double kMidRate = 1.3;
 };
 template <>
 struct TileSet<double> {
