@@ -227,6 +227,20 @@ def test_gram_192_tile_ragged_vs_oracle(native_backend, d, append_ones):
     assert torch.equal(F, F.T)
 
 
+def test_kron_fp32_192_tile_ragged(native_backend):
+    """fp32 factors of a 4000 x 64 gradient with a non-symmetric prior: L
+    (4000², 231 upper tiles of 192², the last row and column of tiles
+    partial) on the 192² tile, R (64²) on the small one."""
+    g = torch.Generator().manual_seed(23)
+    G = torch.randn(4000, 64, generator=g)
+    L0, R0 = torch.randn(4000, 4000, generator=g), torch.randn(64, 64, generator=g)
+    L, R = L0.to(DEV), R0.to(DEV)
+    ops.kron_factor_update_(L, R, G.to(DEV), beta2=0.9)
+    Lo, Ro = oo.kron_factor_update(L0.double().numpy(), R0.double().numpy(), G.double().numpy(), 0.9,
+                                   dtype=np.float64)
+    assert _relfro(_np(L), Lo) <= 1e-5 and _relfro(_np(R), Ro) <= 1e-5
+
+
 def test_kron_bf16_192_tile(native_backend):
     """bf16 factors of a 3000 x 200 gradient: L (3000²) on the 192² tile,
     R (200²) on the small one; vs the float64 oracle at bf16 rounding."""
