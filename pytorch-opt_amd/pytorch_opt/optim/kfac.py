@@ -62,8 +62,9 @@ def damped_inverses_newton(mats, gammas, batch_bytes: int = 4 << 30, power_iters
     for (shape, dev, dt), idx in buckets.items():
         n = shape[-1]
         rdt = torch.float64 if dt == torch.float64 else torch.float32
-        # the root's own workspace holds several n x n matrices per entry
-        step = max(1, batch_bytes // (8 * n * n * torch.finfo(rdt).bits // 8))
+        # the stack and the root's workspace hold about eight n x n matrices
+        # of the root precision per entry
+        step = max(1, batch_bytes // (8 * n * n * (torch.finfo(rdt).bits // 8)))
         eye = torch.eye(n, device=dev, dtype=rdt)
         for s in range(0, len(idx), step):
             chunk = idx[s:s + step]
