@@ -116,6 +116,23 @@ int pto_two_sided_product(const void* A, const void* X, const void* B, void* out
                           int trans_a, int trans_b, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * The same over a batch, each of the two products one launch: out[b] =
+ * op(A[b])*X[b]*op(B[b]) for b < batch (below 65536), A[b] = A + b*stride_a
+ * (elements; 0 shares one matrix across the batch), likewise X and B; out
+ * is contiguous [batch][m][n]. Serves the batched calls of
+ * precond_apply_two_sided and two_sided_product (leading dims of
+ * pytorch_opt/ops/reference.py:117-121, batched there by torch.matmul),
+ * which the harnesses use for same-shape parameters (SOAP rotations,
+ * K-FAC and EKFAC preconditioning, Shampoo's apply). shared_a / shared_b
+ * in the workspace query: the matching stride is 0.
+ */
+size_t pto_two_sided_product_batched_workspace_bytes(int dtype, int64_t batch, int64_t m, int64_t n, int shared_a,
+                                                     int shared_b);
+int pto_two_sided_product_batched(const void* A, const void* X, const void* B, void* out, int dtype, int64_t batch,
+                                  int64_t m, int64_t n, int64_t stride_a, int64_t stride_x, int64_t stride_b,
+                                  int trans_a, int trans_b, void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * One AdamW step of a dense tensor, in place: the shared fallback of the
  * optimizers, pytorch_opt/optim/_common.py:56-79 (torch elementwise ops in
  * the reference; no compiled counterpart). With bc1 = 1 - beta1^step and

@@ -51,6 +51,9 @@ SIGNATURES = {
     "pto_two_sided_product_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
     "pto_two_sided_product": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_int, _c_int,
                                        _c_ptr, _c_size, _c_ptr]),
+    "pto_two_sided_product_batched_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "pto_two_sided_product_batched": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64,
+                                               _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
     "pto_adamw_workspace_bytes": (_c_size, []),
     "pto_adamw_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_dbl, _c_dbl, _c_dbl,
                                 _c_dbl, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
@@ -205,6 +208,9 @@ class HipBackend:
         out_dtype = torch.promote_types(torch.promote_types(A.dtype, X.dtype), B.dtype)
         work = out_dtype if out_dtype in _DTYPE_CODE else torch.float32
         lead = torch.broadcast_shapes(A.shape[:-2], X.shape[:-2], B.shape[:-2])
+        if math.prod(lead) > 1:
+            out = self._two_sided_batched(A.to(work), X.to(work), B.to(work), lead, m, n, trans_a, trans_b, what)
+            return out if out.dtype == out_dtype else out.to(out_dtype)
         Ab = A.to(work).expand(*lead, m, m).reshape(-1, m, m)
         Xb = X.to(work).expand(*lead, m, n).reshape(-1, m, n)
         Bb = B.to(work).expand(*lead, n, n).reshape(-1, n, n)
@@ -225,6 +231,43 @@ class HipBackend:
                 self._check(rc, what)
         out = out.reshape(*lead, m, n)
         return out if out.dtype == out_dtype else out.to(out_dtype)
+
+    # workspace per batched call (packed copies and the intermediate)
+    two_sided_batch_bytes = 4 << 30
+
+    def _two_sided_batched(self, A, X, B, lead, m, n, trans_a, trans_b, what):
+        """op(A)·X·op(B) over the broadcast batch `lead`, one launch per
+        product per chunk; a factor whose leading dims are all 1 is shared
+        (stride 0) instead of copied per matrix."""
+        batch = math.prod(lead)
+
+        def operand(T, r, c):
+            if math.prod(T.shape[:-2]) == 1:
+                return T.reshape(r, c).contiguous(), 0
+            return T.expand(*lead, r, c).reshape(batch, r, c).contiguous(), r * c
+
+        Ab, sa = operand(A, m, m)
+        Xb, sx = operand(X, m, n)
+        Bb, sb = operand(B, n, n)
+        out = torch.empty(batch, m, n, dtype=X.dtype, device=X.device)
+        code = _DTYPE_CODE[X.dtype]
+        with torch.cuda.device(X.device):
+            per = max(1, self._lib.pto_two_sided_product_batched_workspace_bytes(code, 1, m, n, 0, 0))
+            chunk = max(1, min(65535, self.two_sided_batch_bytes // per))
+            stream = self._stream(X.device)
+            for s in range(0, batch, chunk):
+                nb = min(chunk, batch - s)
+                nbytes = self._lib.pto_two_sided_product_batched_workspace_bytes(code, nb, m, n, int(sa == 0),
+                                                                                 int(sb == 0))
+                ws = self._workspace(nbytes, X.device)
+                pa = Ab[s] if sa else Ab
+                px = Xb[s] if sx else Xb
+                pb = Bb[s] if sb else Bb
+                rc = self._lib.pto_two_sided_product_batched(_ptr(pa), _ptr(px), _ptr(pb), _ptr(out[s]), code, nb, m,
+                                                             n, sa, sx, sb, int(trans_a), int(trans_b), _ptr(ws),
+                                                             nbytes, stream)
+                self._check(rc, what)
+        return out.reshape(*lead, m, n)
 
     def adamw_step_(self, p, g, m, v, lr, weight_decay, beta1, beta2, eps, step, return_update_sq):
         tensors = (p, g, m, v)

@@ -372,6 +372,26 @@ def test_two_sided_product_vs_oracle(native_backend, trans, shape):
     assert _relfro(_np(got), want) <= 1e-5
 
 
+@pytest.mark.parametrize("trans", [(False, False), (True, False), (False, True), (True, True)])
+@pytest.mark.parametrize("shapes", [
+    ((5, 96, 96), (5, 96, 200), (5, 200, 200)),    # every factor per matrix
+    ((96, 96), (3, 96, 200), (3, 200, 200)),       # A shared
+    ((4, 256, 256), (4, 256, 384), (384, 384)),    # B shared, unpacked operand paths
+    ((2, 1, 70, 70), (2, 3, 70, 33), (1, 3, 33, 33)),  # broadcast over two leading dims
+])
+def test_two_sided_product_batched_vs_oracle(native_backend, trans, shapes):
+    """Leading dims run as one batched launch per product (shared factors at
+    stride 0), through both ops entry points, against the float64 oracle."""
+    g = torch.Generator().manual_seed(41)
+    A, X, B = (torch.randn(*s, generator=g) for s in shapes)
+    want = oo.two_sided_product(A.double().numpy(), X.double().numpy(), B.double().numpy(), *trans)
+    got = ops.two_sided_product(A.to(DEV), X.to(DEV), B.to(DEV), *trans)
+    assert tuple(got.shape) == want.shape and _relfro(_np(got), want) <= 1e-5
+    if trans == (False, False):
+        got = ops.precond_apply_two_sided(A.to(DEV), X.to(DEV), B.to(DEV))
+        assert _relfro(_np(got), want) <= 1e-5
+
+
 def test_two_sided_product_fp64_bf16_and_rotation(native_backend):
     A, X, B = (torch.randn(s, dtype=torch.float64) for s in [(70, 70), (70, 130), (130, 130)])
     got = ops.two_sided_product(A.to(DEV), X.to(DEV), B.to(DEV), True, True)
