@@ -550,6 +550,59 @@ def test_soap_step_at_size_vs_oracle(native_backend):
     assert np.abs(p.detach().cpu().numpy() - want_p).max() < 5e-5
 
 
+def test_muon_step_at_size_vs_oracle(native_backend):
+    """Two Muon steps of a 1024x4096 fp32 matrix (Nesterov momentum, weight
+    decay, spectral lr factor), each vs the numpy oracle from the same state."""
+    from oracle import optim_oracle as oopt
+    from pytorch_opt import Muon
+
+    torch.manual_seed(43)
+    p = torch.nn.Parameter(0.02 * torch.randn(1024, 4096, device=DEV))
+    opt = Muon([p], lr=0.02, weight_decay=0.01)
+    for _ in range(2):
+        g = 1e-3 * torch.randn(1024, 4096, device=DEV)
+        p.grad = g
+        st = opt.state[p]
+        buf = st["momentum_buffer"].cpu().numpy() if "momentum_buffer" in st else np.zeros((1024, 4096), np.float32)
+        want_p, want_buf, _ = oopt.muon_matrix_step(p.detach().cpu().numpy(), g.cpu().numpy(), buf, lr=0.02,
+                                                    weight_decay=0.01)
+        opt.step()
+        np.testing.assert_allclose(st["momentum_buffer"].cpu().numpy(), want_buf, atol=1e-7)
+        assert np.abs(p.detach().cpu().numpy() - want_p).max() < 1e-5
+
+
+def test_shampoo_step_at_size_vs_oracle(native_backend):
+    """Two Shampoo steps of a 1024x1024 fp32 matrix (EMA factors, fp64
+    coupled-Newton roots refreshed every step, AdaGrad graft), each vs the
+    oracle (float64 eigh roots) from the same state. The factors of a square
+    Gaussian gradient span eigenvalues ~1e-3 to ~4e3; ε = 1 keeps the root's
+    condition near 4e3, so fp32 rounding of the factors (~2e-4 absolute at
+    this scale, in the reference as here) stays out of the comparison."""
+    from oracle import optim_oracle as oopt
+    from pytorch_opt import Shampoo
+
+    torch.manual_seed(44)
+    n = 1024
+    p = torch.nn.Parameter(torch.randn(n, n, device=DEV))
+    kw = dict(lr=0.05, beta2=0.99, eps=1.0, precondition_frequency=1, graft="adagrad")
+    opt = Shampoo([p], max_preconditioner_dim=2048, **kw)
+    for step in range(2):
+        g = torch.randn(n, n, device=DEV)
+        p.grad = g
+        st = opt.state[p]
+        z = np.zeros((n, n), np.float32)
+        L = st["L"].cpu().numpy() if "L" in st else z
+        R = st["R"].cpu().numpy() if "R" in st else z
+        acc = st["graft_acc"].cpu().numpy() if "graft_acc" in st else z
+        want = oopt.shampoo_matrix_step(p.detach().cpu().numpy(), g.cpu().numpy(), L, R, None, None, acc, step,
+                                        st.get("factor_updates", 0), root_method="eigh", **kw)
+        opt.step()
+        np.testing.assert_allclose(st["L"].cpu().numpy(), want[1], rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(st["L_root"].cpu().numpy(), want[3], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(st["R_root"].cpu().numpy(), want[4], rtol=1e-4, atol=1e-5)
+        assert np.abs(p.detach().cpu().numpy() - want[0]).max() < 2e-5
+
+
 def test_kfac_direction_at_size_vs_oracle(native_backend):
     """K-FAC natural gradient of a 1024x(768+1) fp32 layer (factors from 4096
     tokens; eigh and Newton inverses) vs the float64 closed form; EKFAC's
