@@ -240,8 +240,37 @@ class KFAC(Optimizer, DiagnosticsMixin):
                     "and module hooks; fused/functional projections bypass hooks. "
                     "For Mamba-2, use_mem_eff_path=False exposes out_proj.")
 
+    def _precondition_many(self, items):
+        """{name: preconditioned V} for [(name, V)]. K-FAC's same-shape
+        modules share one batched two-sided product (the same per-module
+        arithmetic, one launch per product); subclasses that override
+        _precondition (EKFAC) are called per module."""
+        if type(self)._precondition is not KFAC._precondition:
+            return {name: self._precondition(name, V) for name, V in items}
+        out, buckets = {}, {}
+        for name, V in items:
+            inv = self._inv.get(name)
+            if inv is None:
+                raise RuntimeError(f"Missing K-FAC inverse for {name!r}")
+            key = (tuple(inv["iG"].shape), tuple(V.shape), tuple(inv["iA"].shape), inv["iG"].dtype, V.dtype, V.device)
+            buckets.setdefault(key, []).append((name, V))
+        for group in buckets.values():
+            if len(group) == 1:
+                name, V = group[0]
+                out[name] = self._precondition(name, V)
+                continue
+            iG = torch.stack([self._inv[n]["iG"] for n, _ in group])
+            iA = torch.stack([self._inv[n]["iA"] for n, _ in group])
+            Vs = torch.stack([V.to(iG.dtype) for _, V in group])
+            with torch.autocast(device_type=Vs.device.type, enabled=False):
+                P = ops.precond_apply_two_sided(iG, Vs, iA)
+            for j, (name, V) in enumerate(group):
+                out[name] = P[j].to(V.dtype)
+        return out
+
     def _natural_gradients(self):
         nat = []  # (parameter, its natural-gradient direction)
+        todo = []
         for name, m in self._name_to_module.items():
             w = m.weight
             has_bias = self.tracker.includes_bias(m)
@@ -253,7 +282,10 @@ class KFAC(Optimizer, DiagnosticsMixin):
                 V = torch.cat([gW, gb.unsqueeze(1)], dim=1)
             else:
                 V = gW
-            V = self._precondition(name, V)
+            todo.append((name, m, has_bias, V))
+        pre = self._precondition_many([(name, V) for name, _, _, V in todo])
+        for name, m, has_bias, _ in todo:
+            V, w = pre[name], m.weight
             if w.grad is not None:
                 nat.append((w, (V[:, :-1] if has_bias else V).reshape(w.shape)))
             if has_bias and m.bias.grad is not None:
