@@ -96,7 +96,8 @@ int two_sided_dispatch(const void* Am, const void* X, const void* Bm, void* out,
 int two_sided(const void* Am, const void* X, const void* Bm, void* out, int dtype, int64_t batch, int64_t m, int64_t n,
               int64_t sA, int64_t sX, int64_t sB, bool trans_a, bool trans_b, void* ws, size_t ws_bytes,
               hipStream_t stream, const char* what, const char* left, const char* right) {
-  PTO_REQUIRE(m >= 0 && n >= 0, std::string(what) + ": negative extent");
+  PTO_REQUIRE(m >= 0 && n >= 0 && batch >= 0, std::string(what) + ": negative extent");
+  PTO_REQUIRE(batch * m * n == 0 || (Am && X && Bm && out && ws), std::string(what) + ": null operand or workspace");
   switch (dtype) {
     case kBF16:
       return two_sided_dispatch<bf16>(Am, X, Bm, out, batch, m, n, sA, sX, sB, trans_a, trans_b, ws, ws_bytes, stream,

@@ -110,6 +110,7 @@ size_t pto_kron_workspace_bytes(int dtype, int64_t m, int64_t n) {
 int pto_kron_factor_update(void* L, void* R, const void* G, int dtype, int64_t m, int64_t n, double beta2,
                            void* workspace, size_t ws_bytes, void* stream) {
   PTO_REQUIRE(m >= 0 && n >= 0, "kron_factor_update_: negative extent");
+  PTO_REQUIRE(m * n == 0 || (L && R && G && workspace), "kron_factor_update_: null factor, gradient or workspace");
   PTO_REQUIRE(L != G && R != G, "kron_factor_update_: G must not alias L or R");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
@@ -139,6 +140,8 @@ size_t pto_gram_workspace_bytes(int x_dtype, int64_t rows, int64_t d, int append
 int pto_gram_update(void* F, int f_dtype, const void* X, int x_dtype, int64_t rows, int64_t d, int append_ones,
                     double beta, double alpha, void* workspace, size_t ws_bytes, void* stream) {
   PTO_REQUIRE(rows >= 0 && d >= 0, "gram_update_: negative extent");
+  PTO_REQUIRE((d == 0 && !append_ones) || (F && (rows == 0 || X) && workspace),
+              "gram_update_: null factor, input or workspace");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (x_dtype == pto::kBF16 && f_dtype == pto::kF32)
     return pto::gram_t<pto::bf16, float>(static_cast<float*>(F), static_cast<const pto::bf16*>(X), rows, d,

@@ -283,6 +283,8 @@ int pto_ns5(const void* G, void* out, int dtype, int64_t batch, int64_t rows, in
             double b, double c, double eps, void* workspace, size_t ws_bytes, void* stream) {
   PTO_REQUIRE(batch >= 0 && rows >= 0 && cols >= 0 && steps >= 0,
               "newton_schulz_orthogonalize: negative extent or steps");
+  PTO_REQUIRE(batch * rows * cols == 0 || (G && out && workspace),
+              "newton_schulz_orthogonalize: null input, output or workspace");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case pto::kBF16:

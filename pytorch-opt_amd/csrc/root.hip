@@ -401,6 +401,7 @@ int pto_inverse_root(const void* A, void* out, int dtype, int root_f64, int64_t 
                      double damping, int64_t max_iter, double tol, void* workspace, size_t ws_bytes,
                      int64_t* iters_out, void* stream) {
   PTO_REQUIRE(batch >= 0 && n >= 0 && max_iter >= 0, "inverse_matrix_root: negative extent or max_iter");
+  PTO_REQUIRE(batch * n == 0 || (A && out && workspace), "inverse_matrix_root: null input, output or workspace");
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case pto::kF32:

@@ -58,15 +58,37 @@ def test_version_and_workspace_queries(lib):
 def test_host_side_argument_errors(lib):
     be = _hip.HipBackend(native_build.library_path())
     L = be._lib
-    rc = L.pto_ns5(None, None, 7, 1, 4, 4, 5, 1.0, 1.0, 1.0, 1e-7, None, 0, None)
+    # pointers below are never dereferenced: every call fails its host checks
+    a, b, w = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000), ctypes.c_void_p(0x3000)
+    rc = L.pto_ns5(a, b, 7, 1, 4, 4, 5, 1.0, 1.0, 1.0, 1e-7, w, 0, None)
     assert rc != 0 and b"dtype" in L.pto_last_error()
     rc = L.pto_ns5(None, None, 0, -1, 4, 4, 5, 1.0, 1.0, 1.0, 1e-7, None, 0, None)
     assert rc != 0 and b"negative" in L.pto_last_error()
-    buf = ctypes.c_void_p(0x1000)
-    rc = L.pto_kron_factor_update(buf, ctypes.c_void_p(0x2000), buf, 0, 4, 4, 0.9, None, 0, None)
+    rc = L.pto_kron_factor_update(a, b, a, 0, 4, 4, 0.9, w, 0, None)
     assert rc != 0 and b"alias" in L.pto_last_error()
-    rc = L.pto_gram_update(None, 2, None, 2, 4, 4, 0, 0.0, 1.0, None, 0, None)
+    rc = L.pto_gram_update(a, 2, b, 2, 4, 4, 0, 0.0, 1.0, w, 0, None)
     assert rc != 0 and b"unsupported" in L.pto_last_error()
+
+
+def test_host_side_null_pointers(lib):
+    """A null operand, output or workspace of a non-empty call is an error,
+    not a launch; empty calls accept nulls."""
+    L = _hip.HipBackend(native_build.library_path())._lib
+    a, b, w = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000), ctypes.c_void_p(0x3000)
+    calls = [
+        lambda: L.pto_ns5(None, b, 0, 1, 4, 4, 5, 1.0, 1.0, 1.0, 1e-7, w, 1 << 20, None),
+        lambda: L.pto_ns5(a, b, 0, 1, 4, 4, 5, 1.0, 1.0, 1.0, 1e-7, None, 1 << 20, None),
+        lambda: L.pto_kron_factor_update(None, a, b, 0, 4, 4, 0.9, w, 1 << 20, None),
+        lambda: L.pto_gram_update(None, 0, a, 0, 4, 4, 0, 0.0, 1.0, w, 1 << 20, None),
+        lambda: L.pto_inverse_root(None, b, 0, 0, 1, 4, 4, 0.0, 10, 1e-6, w, 1 << 20, None, None),
+        lambda: L.pto_precond_apply(a, None, a, b, 0, 4, 4, w, 1 << 20, None),
+        lambda: L.pto_two_sided_product(a, a, None, b, 0, 4, 4, 1, 0, w, 1 << 20, None),
+        lambda: L.pto_two_sided_product_batched(a, a, a, None, 0, 2, 4, 4, 16, 16, 16, 0, 0, w, 1 << 20, None),
+    ]
+    for i, call in enumerate(calls):
+        assert call() != 0 and b"null" in L.pto_last_error(), i
+    assert L.pto_ns5(None, None, 0, 0, 4, 4, 5, 1.0, 1.0, 1.0, 1e-7, None, 0, None) == 0
+    assert L.pto_kron_factor_update(None, None, a, 0, 0, 4, 0.9, None, 0, None) == 0
     # workspace too small is caught before any launch
     rc = L.pto_ns5(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000), 0, 1, 64, 64, 5, 1.0, 1.0, 1.0, 1e-7, None, 0,
                    None)
