@@ -667,7 +667,8 @@ int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, c
   g.tiles_n = (g.N + Cfg::BN - 1) / Cfg::BN;
   int64_t tiles = UPPER ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2 : (int64_t)g.tiles_m * g.tiles_n;
   if (tiles == 0 || batch == 0) return 0;
-  PTO_REQUIRE(tiles < (1ll << 31) && batch < 65536, std::string(name) + ": grid too large");
+  // the kernel numbers workgroups across the batch in 32-bit arithmetic
+  PTO_REQUIRE(batch < 65536 && tiles * batch < (1ll << 31), std::string(name) + ": grid too large");
   ProfScope ps(name, stream);
   hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi, QN, PT>), dim3((unsigned)tiles, (unsigned)batch),
                      dim3(Cfg::NT), 0, stream, g, epi);

@@ -55,8 +55,10 @@ void set_error(const std::string& msg);
     }                                                                                \
   } while (0)
 
-// Bump allocator over a caller-provided workspace. Every block is 256-byte
-// aligned so 16-byte vector loads are always legal on workspace operands.
+// Bump allocator over a caller-provided workspace. Every block starts at a
+// 256-byte aligned address, whatever the workspace pointer's alignment, so
+// 16-byte vector loads are always legal on workspace operands; the
+// workspace-size queries include 256 bytes of slack for the first block.
 struct Carver {
   char* base;
   size_t cap;
@@ -66,7 +68,8 @@ struct Carver {
   template <typename T>
   T* take(int64_t count) {
     size_t bytes = static_cast<size_t>(count) * sizeof(T);
-    size_t at = (used + 255) & ~static_cast<size_t>(255);
+    const size_t addr = reinterpret_cast<uintptr_t>(base) + used;
+    size_t at = used + ((256 - (addr & 255)) & 255);
     used = at + bytes;
     if (used > cap || base == nullptr) {
       overflow = true;

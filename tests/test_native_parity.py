@@ -457,6 +457,60 @@ def test_stream_ordering(native_backend):
     assert np.abs(O2.cpu().numpy() - want).max() < 1e-5
 
 
+def test_misaligned_workspace_pointer(native_backend):
+    """A C-ABI caller may pass a workspace that is not 256-byte aligned: the
+    library aligns its blocks itself (within the size the queries return) and
+    the results are bit-identical to an aligned call."""
+    import ctypes
+
+    be = ops._NATIVE
+    L = be._lib
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t, off=0: ctypes.c_void_p(t.data_ptr() + off)  # noqa: E731
+
+    def with_ws(nbytes, call):
+        outs = []
+        for off in (0, 8):
+            raw = torch.empty(nbytes + 8, dtype=torch.uint8, device=DEV)
+            outs.append(call(p(raw, off), nbytes))
+        return outs
+
+    g = torch.Generator(device="cpu").manual_seed(5)
+    G = torch.randn(3, 200, 330, generator=g).to(DEV, torch.bfloat16)
+
+    def ns5(ws, nbytes):
+        out = torch.empty_like(G)
+        assert L.pto_ns5(p(G), p(out), 2, 3, 200, 330, 5, 3.4445, -4.775, 2.0315, 1e-7, ws, nbytes, stream) == 0
+        return out
+
+    a, b = with_ws(L.pto_ns5_workspace_bytes(2, 3, 200, 330), ns5)
+    assert torch.equal(a, b)
+
+    Gk = torch.randn(130, 70, generator=g).to(DEV)
+    Lk0, Rk0 = torch.eye(130, device=DEV), torch.eye(70, device=DEV)
+
+    def kron(ws, nbytes):
+        Lk, Rk = Lk0.clone(), Rk0.clone()
+        assert L.pto_kron_factor_update(p(Lk), p(Rk), p(Gk), 0, 130, 70, 0.9, ws, nbytes, stream) == 0
+        return torch.cat([Lk.flatten(), Rk.flatten()])
+
+    a, b = with_ws(L.pto_kron_workspace_bytes(0, 130, 70), kron)
+    assert torch.equal(a, b)
+
+    A3, X3, B3 = (torch.randn(s, generator=g).to(DEV) for s in ((2, 96, 96), (2, 96, 200), (200, 200)))
+
+    def two_sided(ws, nbytes):
+        out = torch.empty_like(X3)
+        assert L.pto_two_sided_product_batched(p(A3), p(X3), p(B3), p(out), 0, 2, 96, 200, 96 * 96, 96 * 200, 0,
+                                               1, 0, ws, nbytes, stream) == 0
+        return out
+
+    a, b = with_ws(L.pto_two_sided_product_batched_workspace_bytes(0, 2, 96, 200, 0, 1), two_sided)
+    assert torch.equal(a, b)
+    want = torch.matmul(torch.matmul(A3.transpose(-1, -2), X3), B3)
+    assert _relfro(_np(a), _np(want)) < 1e-5
+
+
 # ---------------------------------------------------------------- AdamW
 
 def _adamw_ref_steps(p, grads, lr, wd, betas, eps):
