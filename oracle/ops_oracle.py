@@ -18,8 +18,13 @@ Pinning (tests/test_oracle.py):
                        brute-force outer products
   inverse_root         closed form Q diag(l^(-1/p)) Qᵀ (tests/test_ops_reference.py:16-21),
                        newton ~ eigh (:24-29), damping (:32-38), residual
-  coupled_newton       iteration count and stop rule: golden vectors from
-                       tests/golden when present, else "parity unpinned"
+  coupled_newton       values through inverse_root's closed forms; the stop
+                       rule's iteration count is pinned in float64 (where
+                       convergence, not rounding noise, ends the loop) by the
+                       iteration bound of the quadratic phase; the exact
+                       float32 stopping iteration is noise-driven: "parity
+                       unpinned" for that count (the reference ships no
+                       golden vectors)
   gram_update          brute-force sum of outer products, clone/EMA/mean
   precond_apply        associativity / brute force in float64
   two_sided_product    orthogonal round trip Q·(QᵀXQ)·Qᵀ = X, permutation

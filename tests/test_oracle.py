@@ -142,6 +142,53 @@ def test_inverse_root_closed_form():
         assert 1 <= iters < 100
 
 
+def _scalar_coupled_newton(lam, p, max_iter=100, tol=1e-10):
+    """The coupled Newton iteration of pytorch_opt/ops/reference.py:17-40
+    written per eigenvalue: for A = diag(lam) every matrix in the loop is
+    diagonal, so X, Mk and Mi are lists of scalars and max|Mk - I| is the
+    largest |m - 1|. Returns (x per eigenvalue, iterations)."""
+    import math
+
+    inv_p = 1.0 / p
+    z = (1.0 + p) / (2.0 * math.sqrt(math.fsum(v * v for v in lam)))
+    x = [z ** inv_p] * len(lam)
+    m = [z * v for v in lam]
+    good, good_err, iters = x, None, 0
+    for _ in range(max_iter):
+        iters += 1
+        mi = [(1.0 + inv_p) - inv_p * v for v in m]
+        x = [a * b for a, b in zip(x, mi)]
+        m = [b ** p * v for b, v in zip(mi, m)]
+        err = max(abs(v - 1.0) for v in m)
+        if good_err is not None and err > 1.2 * good_err:
+            return good, iters
+        good, good_err = x, err
+        if err < tol:
+            break
+    return x, iters
+
+
+@pytest.mark.parametrize("p", [1, 2, 3, 4, 6])
+def test_coupled_newton_iteration_count_pinned_in_float64(p):
+    """The oracle's stop rule and iteration count against the eigenvalue-wise
+    recurrence: exact on a diagonal input, and the same count on the rotated
+    one (float64, where convergence rather than rounding noise ends the
+    loop)."""
+    lam = np.logspace(-3, 0, 9)
+    xs, n_scalar = _scalar_coupled_newton(list(lam), p)
+    X, n_oracle = oo.coupled_newton(np.diag(lam), p)
+    assert n_oracle == n_scalar
+    np.testing.assert_allclose(np.diag(X), xs, rtol=1e-12)
+    np.testing.assert_allclose(xs, lam ** (-1.0 / p), rtol=1e-9)
+    Q, _ = np.linalg.qr(np.random.default_rng(p).standard_normal((9, 9)))
+    Xr, n_rot = oo.coupled_newton((Q * lam) @ Q.T, p)
+    assert n_rot == n_scalar
+    np.testing.assert_allclose(Xr, (Q * np.asarray(xs)) @ Q.T, atol=1e-10)
+    # a slower start (eigenvalues spread further) takes more iterations
+    _, n_wide = _scalar_coupled_newton(list(np.logspace(-6, 0, 9)), p)
+    assert n_wide > n_scalar
+
+
 def test_newton_matches_eigh_and_damping():
     # the reference's tests/test_ops_reference.py:24-38
     A, _, _ = _spd(8, 3)
