@@ -149,6 +149,24 @@ def test_ns5_bf16_single_matrix_full_size(native_backend, cols):
     assert float((got.float() - want).norm() / want.norm()) <= 2e-2
 
 
+def test_ns5_bf16_tall_batch_full_size(native_backend):
+    """Rows > cols at full size (4 bf16 matrices of 11008 x 4096, the
+    transposed config-2 shape): the library orthogonalizes Gᵀ and transposes
+    back. Against the reference per matrix, and the transpose identity
+    NS5(Gᵀ) = NS5(G)ᵀ against the row-major run of the same data (only the
+    norm's summation order differs between the two)."""
+    G = _config2_inputs(4, 4096, 11008, 4000)
+    Gt = G.transpose(-1, -2).contiguous()
+    got_t = ops.newton_schulz_orthogonalize(Gt)
+    got = ops.newton_schulz_orthogonalize(G)
+    assert got_t.shape == (4, 11008, 4096) and got_t.dtype == torch.bfloat16
+    for i in range(4):
+        want = ops_ref.newton_schulz_orthogonalize(Gt[i].float())
+        assert float((got_t[i].float() - want).norm() / want.norm()) <= 2e-2
+        d = got_t[i].float() - got[i].float().transpose(0, 1)
+        assert float(d.norm() / got[i].float().norm()) <= 1e-2
+
+
 # ---------------------------------------------------------------- kron
 
 @pytest.mark.parametrize("beta2", [1.0, 0.9, 0.95])
