@@ -173,10 +173,26 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 2) & 3) ^ (r & 2); }
 // column n0 + 4*(s%4); lane s then receives column n0 + s of rows
 // k0..k0+3. With the 16x16x32 MFMA, 16-lane group g holds k = 8g..8g+7,
 // so one read covers rows {4t..4t+3} + 8g and two 16-byte chunks per
-// group. Q rows are 256 or 512 bytes, so a row's banks depend only on the
-// chunk: 16-byte chunk c of Q row r lives at physical chunk c ^ swzq(r),
-// which is distinct (mod 16) across the 8 rows a half-wave reads.
-__device__ __forceinline__ int swzq(int r) { return 2 * ((r & 3) | ((r >> 1) & 4)); }
+// group. A half-wave reads 8 rows ({0..3, 8..11} + 16h, or those plus 4
+// for the second half of a fragment), one 32-byte segment each, and is
+// conflict-free when the 8 segments fall in distinct 32-byte slots of
+// the 256-byte bank row. 16-byte chunk c of Q row r lives at physical
+// chunk c ^ swzq<RB>(r) (an even XOR, so a segment's two chunks stay
+// adjacent):
+//  - rows of a multiple of 256 bytes start at slot 0, and
+//    2·((r & 3) | ((r >> 1) & 4)) spreads the 8 rows over 8 slots;
+//  - rows of 384 bytes (the 192-wide tile) alternate between slots 0 and 4
+//    with r's parity, so the XOR only has to separate the four rows of each
+//    parity: 2·(((r >> 1) & 1) | ((r >> 2) & 2)), which flips chunk bits 1-2
+//    only and so keeps every chunk inside its 128-byte group (below 24).
+// Both depend on row bits 0, 1 and 3 only, so the second half of a
+// fragment (4 rows on) keeps the swizzle.
+template <int RB>
+__device__ __forceinline__ int swzq(int r) {
+  // (the kernel asserts RB % 256 is 0 or 128 wherever the layout is used)
+  if constexpr (RB % 256 == 0) return 2 * ((r & 3) | ((r >> 1) & 4));
+  return 2 * (((r >> 1) & 1) | ((r >> 2) & 2));
+}
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
 
@@ -248,16 +264,16 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   constexpr int PRB = PT ? BM * (int)sizeof(T) : kRowBytes;  // bytes per P row in LDS
   constexpr int CPRP = PRB / 16;                   // 16-byte chunks per P row
   static_assert((BM + BN) % (16 * NW) == 0 && IPW >= 1, "DMA split");
-  static_assert(!PT || (QN && CPRP >= 16 && 1024 % PRB == 0),
-                "PT layout: with QN, P rows of 256 bytes or more dividing 1 KiB");
+  static_assert(!PT || (QN && CPRP >= 16 && (PRB % 256 == 0 || PRB % 256 == 128)),
+                "PT layout: with QN, P rows of 256·k or 256·k + 128 bytes");
   static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0 && WTM % 16 == 0, "wave tile");
   static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
   static_assert(3 * IPW <= 63, "vmcnt range");
   static_assert(Plan::RPP % MF::MN == 0 && WTM % Plan::RPP == 0, "epilogue passes");
   static_assert(kStages * Plan::ARR <= Plan::kLdsMax, "LDS budget");
-  static_assert(!QN || (sizeof(T) == 2 && (!UPPER || PT) && CPR >= 16 && 1024 % QRB == 0 &&
-                        (BM * kRowBytes) % 1024 == 0),
-                "QN layout: bf16, Q rows of 256 bytes or more; symmetric products only with PT");
+  static_assert(!QN || (sizeof(T) == 2 && (!UPPER || PT) && CPR >= 16 && (QRB % 256 == 0 || QRB % 256 == 128) &&
+                        (BM * kRowBytes) % 1024 == 0 && NRG == 1),
+                "QN layout: bf16, Q rows of 256·k or 256·k + 128 bytes; symmetric products only with PT");
 
   if (g.guard != nullptr && *g.guard != 0) return;
 
@@ -283,8 +299,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // Q); lane L supplies bytes 16L..16L+15 of it. In the K-contiguous
   // layout that is row R0 + L/4, physical chunk L%4, i.e. logical chunk
   // (L%4) ^ swz(row); rows past M (N) re-read the last valid row. In the
-  // QN layout a Q lane supplies row rq = byte offset / QRB, physical chunk
-  // L % CPR, logical chunk (L % CPR) ^ swzq(rq); columns past the row
+  // QN layout a Q lane's byte offset o in the Q region gives row
+  // rq = o / QRB, physical chunk (o % QRB) / 16, logical chunk that ^
+  // swzq(rq) (a row may straddle two instructions); columns past the row
   // pitch re-read its last chunk. A PT lane does the same in the P region
   // (rows of PRB bytes, columns from row0).
   const char* src[IPW];
@@ -296,8 +313,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     const int chunk = (lane & 3) ^ swz(r);
     const T* s;
     if (PT && R0 < BM) {
-      const int rp = R0 * kRowBytes / PRB + lane / CPRP;
-      const int c = (lane % CPRP) ^ swzq(rp);
+      const int o = R0 * kRowBytes + 16 * lane;
+      const int rp = o / PRB;
+      const int c = ((o % PRB) >> 4) ^ swzq<PRB>(rp);
       const int64_t col = min((int64_t)row0 + c * VEC, g.ldp - VEC);
       s = static_cast<const T*>(g.P) + (int64_t)b * g.sP + (int64_t)rp * g.ldp + col;
       step[q] = (unsigned)(kRowBytes * g.ldp);
@@ -310,8 +328,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       s = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)gr * g.ldq + chunk * VEC;
       step[q] = kRowBytes;
     } else {
-      const int rq = (R0 - BM) * kRowBytes / QRB + lane / CPR;
-      const int c = (lane % CPR) ^ swzq(rq);
+      const int o = (R0 - BM) * kRowBytes + 16 * lane;
+      const int rq = o / QRB;
+      const int c = ((o % QRB) >> 4) ^ swzq<QRB>(rq);
       const int64_t col = min((int64_t)col0 + c * VEC, g.ldq - VEC);
       s = static_cast<const T*>(g.Q) + (int64_t)b * g.sQ + (int64_t)rq * g.ldq + col;
       step[q] = (unsigned)(kRowBytes * g.ldq);
@@ -347,7 +366,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) {
       const int col = wn * WTN + fn * MF::MN + (lane & (MF::MN - 1) & ~15) + 4 * (li & 3);
-      qoff[fn] = qr * QRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
+      qoff[fn] = qr * QRB + (((col >> 3) ^ swzq<QRB>(qr)) << 4) + ((col & 7) << 1);
     }
   }
   int poff[FM];  // PT: the same for fragment fm of P (columns = rows of the output)
@@ -356,7 +375,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
       const int col = wm * WTM + fm * MF::MN + (lane & (MF::MN - 1) & ~15) + 4 * (li & 3);
-      poff[fm] = qr * PRB + (((col >> 3) ^ swzq(qr)) << 4) + ((col & 7) << 1);
+      poff[fm] = qr * PRB + (((col >> 3) ^ swzq<PRB>(qr)) << 4) + ((col & 7) << 1);
     }
   }
   // One K tile's MFMA operands for this wave.
@@ -648,19 +667,6 @@ inline int device_cus() {
   return n;
 }
 
-// Tiles are spread over the CUs, so the product ends when the busiest CU has
-// run ceil(tiles / CUs) of them. Pick the tile size whose busiest CU covers
-// the least area after weighting by the big tile's higher rate. At the same
-// number of tiles per CU the big tile wins; a big tiling that leaves half
-// the CUs idle (e.g. 64 big tiles against 256 small ones) loses.
-template <typename T, class Big, class Small>
-bool prefer_big_tiles(int64_t big_tiles, int64_t small_tiles) {
-  const int64_t cus = device_cus();
-  const double big_load = double((big_tiles + cus - 1) / cus) * (Big::BM * Big::BN);
-  const double small_load = double((small_tiles + cus - 1) / cus) * (Small::BM * Small::BN);
-  return big_load < small_load * TileSet<T>::kBigRate;
-}
-
 template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false>
 int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
   g.tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
@@ -687,8 +693,13 @@ struct PickTiles<T, true> {
   typedef typename TileSet<T>::sym_small Small;
 };
 
-// The same model over the big, small and (symmetric bf16) mid tiles of
-// launch_gemm: 0 = small, 1 = big, 2 = mid.
+// Tiles are spread over the CUs, so the product ends when the busiest CU has
+// run ceil(tiles / CUs) of them. Pick the tile size whose busiest CU covers
+// the least area after weighting each size by its measured rate (small 1.0,
+// big kBigRate, the symmetric 192² tile kMidRate). At the same number of
+// tiles per CU the big tile wins; a big tiling that leaves half the CUs
+// idle (e.g. 64 big tiles against 256 small ones) loses. Returns 0 = small,
+// 1 = big, 2 = mid.
 template <typename T, bool UPPER>
 int pick_tile(int64_t M, int64_t N, int64_t batch) {
   typedef typename PickTiles<T, UPPER>::Big Big;
@@ -754,12 +765,14 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
   PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 && (!PT || (g.ldp >= g.M && g.ldp >= 8)) &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
-  const int64_t tm = (g.M + Big::BM - 1) / Big::BM, tn = (g.N + Big::BN - 1) / Big::BN;
-  const int64_t sm = (g.M + Small::BM - 1) / Small::BM, sn = (g.N + Small::BN - 1) / Small::BN;
-  const int64_t big_tiles = (UPPER ? tm * (tm + 1) / 2 : tm * tn) * batch;
-  const int64_t small_tiles = (UPPER ? sm * (sm + 1) / 2 : sm * sn) * batch;
-  if (prefer_big_tiles<bf16, Big, Small>(big_tiles, small_tiles))
-    return launch_gemm_cfg<bf16, Big, UPPER, Epi, true, PT>(g, epi, batch, stream, name);
+  const int pick = pick_tile<bf16, UPPER>(g.M, g.N, batch);
+  if constexpr (UPPER) {
+    // the 192² tile: 384-byte transposing rows (swzq's second form)
+    typedef typename TileSet<bf16>::sym_mid Mid;
+    static_assert(Mid::BM == Mid::BN && Mid::BK == Big::BK, "mid tile: square, same K tile");
+    if (pick == 2) return launch_gemm_cfg<bf16, Mid, UPPER, Epi, true, PT>(g, epi, batch, stream, name);
+  }
+  if (pick == 1) return launch_gemm_cfg<bf16, Big, UPPER, Epi, true, PT>(g, epi, batch, stream, name);
   return launch_gemm_cfg<bf16, Small, UPPER, Epi, true, PT>(g, epi, batch, stream, name);
 }
 

@@ -220,17 +220,14 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
       GemmArgs g{Ab, ldm, sAB, Ab, ldm, sAB, (int)m, (int)m, (int)ldm, 0, 0, nullptr};
       EpiNsSq<T, A> e{Ab, Bb, ldm, sAB, static_cast<A>(a), static_cast<A>(b), static_cast<A>(c),
                       vec_ok<T>(Ab, ldm, sAB) && vec_ok<T>(Bb, ldm, sAB)};
-      // A is symmetric: both operands read as its own transpose (PT), unless
-      // the 192² tile fits the launch better (it exists for K-contiguous
-      // reads only; A's rows are its columns, so the NT launch reads A too)
-      bool launched = false;
+      // A is symmetric: both operands read as its own transpose (PT), on
+      // any of the three symmetric tiles; without the transposing reads
+      // (fp32, fp64) A's rows are its columns, so the NT launch reads A too
       if constexpr (QN) {
-        if (pick_tile<T, true>(m, m, nb) != 2) {
-          if (launch_gemm_qn<EpiNsSq<T, A>, true, true>(g, e, nb, stream, "ns5_square")) return -1;
-          launched = true;
-        }
+        if (launch_gemm_qn<EpiNsSq<T, A>, true, true>(g, e, nb, stream, "ns5_square")) return -1;
+      } else {
+        if (launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
       }
-      if (!launched && launch_gemm<T, true>(g, e, nb, stream, "ns5_square")) return -1;
     }
     // 3. X' = B'·X   (QN: over X itself; else as B'·(Xᵀ)ᵀ over the stored
     //    transpose, X written in place since this product does not read it)
