@@ -13,8 +13,11 @@
  *    arguments are `batch` matrices laid out back to back.
  *  - `dtype` is one of PTO_F32, PTO_F64, PTO_BF16.
  *  - `workspace` is caller-owned device memory of at least the size the
- *    matching *_workspace_bytes query returns. The library never allocates
- *    device memory and keeps no state between calls.
+ *    matching *_workspace_bytes query returns, at any alignment (the
+ *    library aligns its blocks inside it; the sizes include that slack).
+ *    The library never allocates device memory and keeps no state between
+ *    calls. A null operand, output or workspace of a non-empty call is an
+ *    error reported before any launch.
  *  - `stream` is a hipStream_t; all kernels are enqueued on it and the call
  *    returns without synchronising, except pto_inverse_root, which reads
  *    its stop flag back once per chunk of iterations (the reference syncs
