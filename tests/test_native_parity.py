@@ -88,6 +88,23 @@ def test_ns5_bf16_vs_oracle(native_backend, shape):
     assert _relfro(_np(got), want) <= 2e-2
 
 
+@pytest.mark.parametrize("shape", [(3000, 3100), (3500, 3000), (2900, 2900)])
+def test_ns5_bf16_192_tile_ragged(native_backend, shape):
+    """Single bf16 matrices whose symmetric products run on the 192² tile
+    with a partial last tile row (3000 = 15·192 + 120; 2900 = 15·192 + 20):
+    the gram's K-contiguous reads and the square's 384-byte transposing
+    reads both clamp at the padded edge. Against the package's pure-torch
+    fp32 reference on the GPU and, for the first shape, the oracle."""
+    g = torch.Generator(device="cpu").manual_seed(sum(shape))
+    G = (torch.randn(*shape, generator=g) * 1e-3).bfloat16()
+    got = ops.newton_schulz_orthogonalize(G.to(DEV))
+    want = ops_ref.newton_schulz_orthogonalize(G.to(DEV).float())
+    assert got.dtype == torch.bfloat16 and got.shape == G.shape
+    assert float((got.float() - want).norm() / want.norm()) <= 2e-2
+    if shape == (3000, 3100):
+        assert _relfro(_np(got), oo.ns5(G.float().numpy())) <= 2e-2
+
+
 @pytest.mark.parametrize("coeffs", [(1.5, -0.5, 0.0), (3.0, -3.2, 1.2), (2.0, 0.0, -0.25)])
 def test_ns5_bf16_coefficient_forms(native_backend, coeffs):
     """bf16 batches with other coefficient sets: cubic Newton–Schulz (c = 0),
