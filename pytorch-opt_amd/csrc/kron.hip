@@ -85,6 +85,20 @@ int gram_t(TF* F, const TX* X, int64_t rows, int64_t d, int append_ones, double 
   Carver cv(ws, ws_bytes);
   TX* XT = cv.take<TX>(dd * ldr);
   PTO_REQUIRE(!cv.overflow, "gram_update_: workspace too small");
+  // bf16 X without the ones column is already the [K][M] operand of the
+  // transposing-read layout (K = tokens, M = features), for both sides of
+  // X̃ᵀX̃: read it in place, no Xᵀ pass, when the token count needs no pad
+  // rows and the rows are whole 16-byte chunks. The 256² tile would spill
+  // with the fp32 blend epilogue on this layout, so only the 192² and 128²
+  // tiles take it.
+  if constexpr (sizeof(TX) == 2) {
+    if (!append_ones && rows % kPadK == 0 && d % 8 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
+        pick_tile<TX, true>(dd, dd, 1) != 1) {
+      GemmArgs g{X, d, 0, X, d, 0, (int)dd, (int)dd, (int)rows, 0, 0, nullptr};
+      EpiBlend<TF, A> e{F, dd, 0, static_cast<A>(beta), static_cast<A>(alpha), vec_ok<TF>(F, dd, 0)};
+      return launch_gemm_qn<EpiBlend<TF, A>, true, true>(g, e, 1, stream, "gram_update");
+    }
+  }
   // X̃ᵀ, [dd][ldr], with the ones row appended and the token pad zeroed.
   if (launch_pack<TX, TX, A>(X, rows, d, d, 0, nullptr, nullptr, 0, 0, XT, ldr, 0, append_ones != 0, 1, stream))
     return -1;

@@ -244,6 +244,24 @@ def test_gram_vs_oracle(native_backend, append_ones):
     assert _relfro(_np(F), want) <= 1e-6
 
 
+@pytest.mark.parametrize("rows, d", [(256, 200), (1024, 3000), (2048, 2048)])
+def test_gram_direct_transposing_reads_vs_oracle(native_backend, rows, d):
+    """bf16 X with a token count that is a multiple of 128, a width that is
+    a multiple of 8 and no ones column is read in place as the transposing
+    operand on both sides (128² tiles for d = 200 and 2048, 192² tiles with
+    a partial last tile row for d = 3000): EMA blend vs the oracle."""
+    g = torch.Generator(device="cpu").manual_seed(rows + d)
+    X = torch.randn(rows, d, generator=g).bfloat16()
+    F0 = torch.randn(d, d, generator=g)
+    F0 = (F0 + F0.T) / 2
+    F = F0.to(DEV)
+    ops.gram_update_(F, X.to(DEV), beta=0.9, alpha=0.1 / rows, append_ones=False)
+    want = oo.gram_update(F0.numpy(), X.float().numpy(), 0.9, 0.1 / rows, False, dtype=np.float64)
+    assert _relfro(_np(F), want) <= 1e-5
+    Fs = _np(F)
+    assert np.array_equal(Fs, Fs.T)
+
+
 @pytest.mark.parametrize("d, append_ones", [(4000, True), (3900, False)])
 def test_gram_192_tile_ragged_vs_oracle(native_backend, d, append_ones):
     """A single d ≈ 4000 factor takes the 192² symmetric tile (one round of
