@@ -95,6 +95,22 @@ int pto_inverse_root(const void* A, void* out, int dtype, int root_f64, int64_t 
                      int64_t* iters_out, void* stream);
 
 /*
+ * The same iteration over a stack of independent matrices, each run by its
+ * own rule: its own err, divergence guard, stop and returned iterate, so
+ * out[b] and iters_out[b] (int64_t[batch], may be NULL) equal what one
+ * pto_inverse_root call on matrix b alone returns. The reference calls
+ * inverse_matrix_root once per factor (pytorch_opt/optim/shampoo.py:112-117);
+ * this is that loop in one launch sequence, for callers that stack
+ * same-shape factors. pto_inverse_root keeps the reference's batch-wide
+ * rule for a batched A (pytorch_opt/ops/reference.py:34, one amax over all
+ * dims). batch * max_iter must stay below 2^31.
+ */
+size_t pto_inverse_root_each_workspace_bytes(int root_f64, int64_t batch, int64_t n, int64_t max_iter);
+int pto_inverse_root_each(const void* A, void* out, int dtype, int root_f64, int64_t batch, int64_t n, int64_t p,
+                          double damping, int64_t max_iter, double tol, void* workspace, size_t ws_bytes,
+                          int64_t* iters_out, void* stream);
+
+/*
  * Two-sided preconditioner application. Replaces
  *   _NATIVE.precond_apply_two_sided(L_root, G, R_root)
  * called at pytorch_opt/ops/__init__.py:83; semantics of

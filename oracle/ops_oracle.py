@@ -99,10 +99,12 @@ def kron_factor_update(L, R, G, beta2=1.0, dtype=None):
     return L * bb + aa * left, R * bb + aa * right
 
 
-def coupled_newton(M, p, max_iter=100, tol=1e-10):
+def coupled_newton(M, p, max_iter=100, tol=1e-10, matmul=np.matmul):
     """Coupled Newton for M^(-1/p) — pytorch_opt/ops/reference.py:17-40.
 
     Returns (X, iterations executed). M is [..., n, n] in the root dtype.
+    ``matmul`` computes every product (a test can change the summation
+    order; the default is numpy's BLAS).
     """
     dt = M.dtype.type
     n = M.shape[-1]
@@ -118,8 +120,8 @@ def coupled_newton(M, p, max_iter=100, tol=1e-10):
     for _ in range(max_iter):
         iters += 1
         Mi = dt(1.0 + inv_p) * eye + dt(-inv_p) * Mk
-        X = X @ Mi
-        Mk = matrix_power(Mi, p) @ Mk
+        X = matmul(X, Mi)
+        Mk = matmul(matrix_power(Mi, p, matmul), Mk)
         err = np.max(np.abs(Mk - eye))
         if good_err is not None and err > good_err * dt(1.2):
             return good, iters
@@ -129,29 +131,31 @@ def coupled_newton(M, p, max_iter=100, tol=1e-10):
     return X, iters
 
 
-def matrix_power(A, p):
+def matrix_power(A, p, matmul=np.matmul):
     """A**p with the product order of torch.linalg.matrix_power: direct for
     p <= 3, else binary powering from the least significant bit."""
     if p == 1:
         return A.copy()
     if p == 2:
-        return A @ A
+        return matmul(A, A)
     if p == 3:
-        return (A @ A) @ A
+        return matmul(matmul(A, A), A)
     z = res = None
     k = p
     while k > 0:
         bit, k = k & 1, k >> 1
-        z = A if z is None else z @ z
+        z = A if z is None else matmul(z, z)
         if bit:
-            res = z if res is None else res @ z
+            res = z if res is None else matmul(res, z)
     return res
 
 
-def inverse_root(A, p, damping=0.0, method="auto", root_dtype=np.float64, max_iter=100, tol=1e-10):
+def inverse_root(A, p, damping=0.0, method="auto", root_dtype=np.float64, max_iter=100, tol=1e-10,
+                 matmul=np.matmul):
     """(A + damping·I)^(-1/p) — pytorch_opt/ops/reference.py:43-68.
 
-    Returns (root in the input dtype, iterations; 0 for eigh).
+    Returns (root in the input dtype, iterations; 0 for eigh). ``matmul``
+    as in coupled_newton.
     """
     if int(p) != p or p < 1:
         raise ValueError(f"p must be a positive integer, got {p}")
@@ -162,7 +166,7 @@ def inverse_root(A, p, damping=0.0, method="auto", root_dtype=np.float64, max_it
     if damping:
         M = M + root_dtype(damping) * np.eye(M.shape[-1], dtype=root_dtype)
     if method == "newton":
-        X, iters = coupled_newton(M, int(p), max_iter, tol)
+        X, iters = coupled_newton(M, int(p), max_iter, tol, matmul)
     else:
         lam, V = np.linalg.eigh(M)
         lam = np.maximum(lam, 1e-30)

@@ -62,15 +62,21 @@ def adamw_step(p, g, m, v, t, lr, betas=(0.9, 0.95), eps=1e-8, wd=0.0):
 
 def shampoo_matrix_step(p, g, L, R, L_root, R_root, graft_acc, step, factor_updates, lr=0.03, beta2=0.999,
                         eps=1e-8, precondition_frequency=20, graft="adagrad", diag_eps=1e-10, root_dtype=np.float64,
-                        root_method="auto"):
+                        root_method="auto", factors=None, roots=None):
     """One Shampoo update of a selected matrix (no momentum / wd / bootstrap).
 
-    Returns the new (p, L, R, L_root, R_root, graft_acc).
+    Returns the new (p, L, R, L_root, R_root, graft_acc). Teacher forcing
+    per stage: ``factors`` = (L, R) after this step's update replaces the
+    oracle's own factor update, ``roots`` = (L_root, R_root) this step's
+    roots (on a refresh step), so each stage can start from a GPU run's
+    result of the stage before.
     """
     g2 = g.reshape(g.shape[0], -1)
-    L, R = oo.kron_factor_update(L, R, g2, beta2)
+    L, R = oo.kron_factor_update(L, R, g2, beta2) if factors is None else factors
     factor_updates += 1
-    if step % precondition_frequency == 0:
+    if roots is not None and step % precondition_frequency == 0:
+        L_root, R_root = roots
+    elif step % precondition_frequency == 0:
         bc = 1.0 - beta2 ** factor_updates if beta2 < 1.0 else 1.0
         L_root = oo.inverse_root(L / np.float32(bc), 4, damping=eps, method=root_method, root_dtype=root_dtype)[0]
         R_root = oo.inverse_root(R / np.float32(bc), 4, damping=eps, method=root_method, root_dtype=root_dtype)[0]

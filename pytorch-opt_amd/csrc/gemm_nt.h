@@ -106,7 +106,8 @@ struct GemmArgs {
   int64_t ldq, sQ;
   int M, N, K;
   int tiles_m, tiles_n;
-  const int* guard;  // if non-null and *guard != 0 the launch does nothing
+  const int* guard;  // if non-null and guard[b * guard_stride] != 0, matrix b is skipped
+  int guard_stride;  // ints between the guard words of consecutive matrices (0: one word)
 };
 
 // Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each
@@ -244,7 +245,7 @@ struct LdsPlan {
 // symmetric P (B' in X' = B'·X, A in A·A) that is P itself: its rows are
 // its columns, so the product reads it with conflict-free transposing LDS
 // reads and 512-byte DMA rows instead of 16-byte row chunks.
-template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false>
+template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false, bool COMP = false>
 __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   typedef Mfma<T> MF;
   typedef typename MF::cvec_t cvec_t;
@@ -275,8 +276,6 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
                         (BM * kRowBytes) % 1024 == 0 && NRG == 1),
                 "QN layout: bf16, Q rows of 256·k or 256·k + 128 bytes; symmetric products only with PT");
 
-  if (g.guard != nullptr && *g.guard != 0) return;
-
   __shared__ __attribute__((aligned(16))) char st0[Plan::ARR];
   __shared__ __attribute__((aligned(16))) char st1[Plan::ARR];
   __shared__ __attribute__((aligned(16))) char st2[Plan::ARR];
@@ -290,6 +289,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const int ntile = gridDim.x;  // tiles per matrix
   const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y);
   const int b = logical / ntile;
+  if (g.guard != nullptr && g.guard[(int64_t)b * g.guard_stride] != 0) return;
   int ti, tj;
   decode_tile<UPPER>(logical - b * ntile, g.tiles_m, g.tiles_n, ti, tj);
   const int row0 = ti * BM, col0 = tj * BN;
@@ -426,15 +426,47 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       }
     }
   };
+  // COMP (fp32 only): blocked accumulation. gfx950's fp32 MFMA rounds
+  // after every k (its results match a sequential FMA chain bit for bit,
+  // as hipBLASLt's do), so one accumulator over all of K carries ~sqrt(K)
+  // roundings. With COMP each K tile's 16 products form a fresh chain of
+  // four MFMAs and the tile sums are added into the accumulator, which
+  // cuts the relative error of a 1024-deep product from 5.7e-7 to 1.6e-7
+  // (4096-deep: 1.1e-6 to 3.0e-7), below a cache-blocked CPU sgemm's. The
+  // coupled Newton root, whose fp32 iterate amplifies product rounding in
+  // ill-conditioned directions, uses it; the extra adds cost 7-25% on
+  // other fp32 products, which keep the plain chain.
+  constexpr bool kComp = COMP && std::is_same<T, float>::value;
   auto mma = [&](const Frag& f) {
+    if constexpr (kComp) {
+      // one row of FN chains at a time, interleaved, so consecutive MFMAs
+      // are independent
 #pragma unroll
-    for (int rg = 0; rg < NRG; ++rg)
+      for (int fm = 0; fm < FM; ++fm) {
+        cvec_t t[FN];
 #pragma unroll
-      for (int ii = 0; ii < IPR; ++ii)
+        for (int rg = 0; rg < NRG; ++rg)
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
+          for (int ii = 0; ii < IPR; ++ii)
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MF::mma(f.a[rg][fm], f.b[rg][fn], ii, acc[fm][fn]);
+            for (int fn = 0; fn < FN; ++fn)
+              t[fn] = MF::mma(f.a[rg][fm], f.b[rg][fn], ii, (rg | ii) ? t[fn] : cvec_t{0, 0, 0, 0});
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+#pragma unroll
+          for (int r = 0; r < MF::NACC; ++r) acc[fm][fn][r] += t[fn][r];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int rg = 0; rg < NRG; ++rg)
+#pragma unroll
+        for (int ii = 0; ii < IPR; ++ii)
+#pragma unroll
+          for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = MF::mma(f.a[rg][fm], f.b[rg][fn], ii, acc[fm][fn]);
+    }
   };
 
   // Skewed pipeline: during step s the wave issues the LDS reads of tile
@@ -667,7 +699,7 @@ inline int device_cus() {
   return n;
 }
 
-template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false>
+template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT = false, bool COMP = false>
 int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
   g.tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
   g.tiles_n = (g.N + Cfg::BN - 1) / Cfg::BN;
@@ -676,7 +708,7 @@ int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, c
   // the kernel numbers workgroups across the batch in 32-bit arithmetic
   PTO_REQUIRE(batch < 65536 && tiles * batch < (1ll << 31), std::string(name) + ": grid too large");
   ProfScope ps(name, stream);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi, QN, PT>), dim3((unsigned)tiles, (unsigned)batch),
+  hipLaunchKernelGGL((gemm_nt_kernel<T, Cfg, UPPER, Epi, QN, PT, COMP>), dim3((unsigned)tiles, (unsigned)batch),
                      dim3(Cfg::NT), 0, stream, g, epi);
   PTO_LAUNCHED(name);
   return 0;
@@ -722,8 +754,9 @@ int pick_tile(int64_t M, int64_t N, int64_t batch) {
   return pick;
 }
 
-// Validate the operand contract and pick a tile size.
-template <typename T, bool UPPER, class Epi>
+// Validate the operand contract and pick a tile size. COMP: blocked fp32
+// accumulation (see the main loop).
+template <typename T, bool UPPER, class Epi, bool COMP = false>
 int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
   typedef typename PickTiles<T, UPPER>::Big Big;
   typedef typename PickTiles<T, UPPER>::Small Small;
@@ -739,10 +772,10 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
   if constexpr (UPPER && TileSet<T>::kHasMid) {
     typedef typename TileSet<T>::sym_mid Mid;
     static_assert(Mid::BM == Mid::BN && Mid::BK == Big::BK, "mid tile: square, same K tile");
-    if (pick == 2) return launch_gemm_cfg<T, Mid, UPPER, Epi>(g, epi, batch, stream, name);
+    if (pick == 2) return launch_gemm_cfg<T, Mid, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
   }
-  if (pick == 1) return launch_gemm_cfg<T, Big, UPPER, Epi>(g, epi, batch, stream, name);
-  return launch_gemm_cfg<T, Small, UPPER, Epi>(g, epi, batch, stream, name);
+  if (pick == 1) return launch_gemm_cfg<T, Big, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
+  return launch_gemm_cfg<T, Small, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
 }
 
 // C[b](i,j) = sum_k P[b](i,k) * Q[b](k,j) with Q stored [K][N] (row pitch

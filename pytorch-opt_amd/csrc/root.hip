@@ -9,16 +9,26 @@
 //     Mi = (1 + 1/p)·I − Mk/p;  X = X·Mi;  Mk = Mi^p·Mk;  err = max|Mk − I|
 //     stop keeping the previous X if err > 1.2·previous err; stop if err < tol
 //   return sym(X) in the input dtype
-// `err` is one maximum over the whole batch, as in the reference.
+// `err` is one maximum over the whole batch, as in the reference's batched
+// call. pto_inverse_root_each instead runs every matrix of the batch by its
+// own rule (own err, divergence guard, stop and returned iterate), exactly
+// as one call per matrix would: the optimizers stack independent factors
+// into one launch sequence that way.
 //
 // Symmetric formulation. In exact arithmetic X, Mk, Mi and every power of
-// Mi are symmetric (all are polynomials in M). Here Mi^p and Mi^p·Mk (and
-// in fp64 also X·Mi) are symmetric by construction: computed on upper
-// tiles only and mirrored. That halves their MFMA work and is also what
+// Mi are symmetric (all are polynomials in M). Here X·Mi, Mi^p and Mi^p·Mk
+// are symmetric by construction: computed on upper tiles only and
+// mirrored. That halves their MFMA work and is also what
 // keeps fp32 stable: with full products (the reference's form) but
 // symmetrised powers, Mk's antisymmetric rounding part is never corrected
 // and X drifts; with Mk kept symmetric the iteration converges like the
 // reference's (same err floor) with a smaller final residual.
+//
+// fp32 products accumulate in blocks (the GEMM core's COMP mode): at
+// cond ~1e6 the returned iterate's residual is set by product rounding in
+// the small-eigenvalue directions (a plain fp32 MFMA chain over K, which
+// rounds like a sequential FMA loop, ends config-size runs at 2-10x the
+// residual of the blocked sums).
 //
 // Device-side control: every kernel of an iteration checks a device flag
 // and exits at once after the stop decision, and a one-thread kernel makes
@@ -28,6 +38,7 @@
 // divergence guard fires.
 #include <algorithm>
 #include <limits>
+#include <vector>
 
 #include "aux_kernels.h"
 #include "gemm_nt.h"
@@ -35,6 +46,9 @@
 namespace pto {
 namespace {
 
+// Stop state of one iteration run. Global mode: one state. Per-matrix
+// mode: state 0 summarises (stopped once every matrix has stopped; iters =
+// loop iterations run) and state 1 + b belongs to matrix b.
 template <typename R>
 struct RootState {
   int stopped;
@@ -43,6 +57,8 @@ struct RootState {
   int pad;
   R prev_err;
 };
+static_assert(sizeof(RootState<float>) % sizeof(int) == 0 && sizeof(RootState<double>) % sizeof(int) == 0,
+              "state stride in ints");
 
 template <typename R>
 struct Bits;
@@ -127,8 +143,8 @@ __global__ void root_init_kernel(const R* __restrict__ M, int64_t n, int64_t ld,
 }
 
 // Epilogue of Mk' = Mi^p·Mk (upper tiles + mirror): writes Mk' and the next
-// Mi and folds max|Mk' − I| into err (bitwise max of non-negative values,
-// which keeps NaN).
+// Mi and folds max|Mk' − I| into err[b * err_stride] (bitwise max of
+// non-negative values, which keeps NaN; err_stride 0 = one batch maximum).
 template <typename R>
 struct EpiMk {
   typedef R S;
@@ -137,6 +153,7 @@ struct EpiMk {
   int64_t ld, sb;
   R c1, alpha;
   typename Bits<R>::U* err;
+  int err_stride;
   typename Bits<R>::U mx;
   bool vec;
   typedef NoPre Pre;
@@ -173,38 +190,63 @@ struct EpiMk {
   __device__ __forceinline__ void put_t(int b, int j, int i0, const R* v, int n, const PreT&) {
     run(b, j, i0, v, 0, n);
   }
-  __device__ __forceinline__ void finish(int) {
+  __device__ __forceinline__ void finish(int b) {
     for (int off = 32; off > 0; off >>= 1) {
       typename Bits<R>::U o = __shfl_xor(mx, off, 64);
       mx = o > mx ? o : mx;
     }
-    if ((threadIdx.x & 63) == 0) atomicMax(err, mx);
+    if ((threadIdx.x & 63) == 0) atomicMax(err + (int64_t)b * err_stride, mx);
   }
 };
 
+// The stop rule for one run after loop iteration `it` with error e.
 template <typename R>
-__global__ void root_decide_kernel(RootState<R>* st, const R* __restrict__ err, int it, R tol) {
-  if (threadIdx.x != 0 || st->stopped) return;
-  R e = err[it];
-  st->iters = it + 1;
-  if (it > 0 && e > st->prev_err * R(1.2)) {  // diverging: keep the last good iterate
-    st->stopped = 1;
-    st->result = it;
+__device__ void decide_one(RootState<R>& st, R e, int it, R tol) {
+  if (st.stopped) return;
+  st.iters = it + 1;
+  if (it > 0 && e > st.prev_err * R(1.2)) {  // diverging: keep the last good iterate
+    st.stopped = 1;
+    st.result = it;
   } else {
-    st->prev_err = e;
-    st->result = it + 1;
-    if (e < tol) st->stopped = 1;
+    st.prev_err = e;
+    st.result = it + 1;
+    if (e < tol) st.stopped = 1;
+  }
+}
+
+// Global mode: one thread applies the rule to err[it]. Per-matrix mode: the
+// block applies it to each matrix (err[it·nb + b]) and then to the summary.
+template <typename R>
+__global__ void __launch_bounds__(256) root_decide_kernel(RootState<R>* st, const R* __restrict__ err, int it, R tol,
+                                                          int nb, int each) {
+  if (!each) {
+    if (threadIdx.x == 0) decide_one(st[0], err[it], it, tol);
+    return;
+  }
+  __shared__ int live;
+  if (threadIdx.x == 0) live = 0;
+  __syncthreads();
+  int mine = 0;
+  for (int b = threadIdx.x; b < nb; b += blockDim.x) {
+    decide_one(st[1 + b], err[(int64_t)it * nb + b], it, tol);
+    mine |= !st[1 + b].stopped;
+  }
+  if (mine) atomicOr(&live, 1);
+  __syncthreads();
+  if (threadIdx.x == 0 && !st[0].stopped) {
+    st[0].iters = it + 1;
+    if (!live) st[0].stopped = 1;
   }
 }
 
 // out = sym(X_result) cast to the input dtype.
 template <typename R, typename TO>
 __global__ void __launch_bounds__(256) root_final_kernel(const R* __restrict__ X0, const R* __restrict__ X1,
-                                                         const RootState<R>* st, int64_t n, int64_t ld, int64_t sb,
-                                                         TO* __restrict__ out) {
+                                                         const RootState<R>* st, int each, int64_t n, int64_t ld,
+                                                         int64_t sb, TO* __restrict__ out) {
   __shared__ R t1[32][33], t2[32][33];
-  const R* X = (st->result & 1) ? X1 : X0;
   const int b = blockIdx.z;
+  const R* X = (st[each ? 1 + b : 0].result & 1) ? X1 : X0;
   const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
   const R* Xb = X + (int64_t)b * sb;
   const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
@@ -224,27 +266,31 @@ __global__ void __launch_bounds__(256) root_final_kernel(const R* __restrict__ X
 
 constexpr int kRootBufs = 10;
 
+// each: per-matrix stop mode (err slots and states per matrix).
 template <typename R>
-size_t root_ws_bytes_t(int64_t batch, int64_t n, int64_t max_iter) {
+size_t root_ws_bytes_t(int64_t batch, int64_t n, int64_t max_iter, bool each) {
   int64_t ld = round_up(n, kPadK);
   size_t bytes = 0;
   auto add = [&](size_t b) { bytes = round_up(bytes, 256) + b; };
   add(sizeof(double) * kRedBlocks * batch);
   add(sizeof(R) * batch);
   add(sizeof(R) * batch);
-  add(sizeof(R) * std::max<int64_t>(max_iter, 1));
-  add(sizeof(RootState<R>));
+  add(sizeof(R) * std::max<int64_t>(max_iter, 1) * (each ? batch : 1));
+  add(sizeof(RootState<R>) * (each ? 1 + batch : 1));
   for (int i = 0; i < kRootBufs; ++i) add(sizeof(R) * batch * n * ld);
   return bytes + 256;
 }
 
+// iters_out: one count (global mode) or one per matrix (each).
 template <typename TI, typename R>
 int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double damping, int64_t max_iter, double tol,
-           void* ws, size_t ws_bytes, int64_t* iters_out, hipStream_t stream) {
+           bool each, void* ws, size_t ws_bytes, int64_t* iters_out, hipStream_t stream) {
   typedef typename Bits<R>::U U;
   PTO_REQUIRE(p >= 1, "inverse_matrix_root: p must be a positive integer");
-  PTO_REQUIRE(n <= INT32_MAX && batch <= 65535 && max_iter <= INT32_MAX, "inverse_matrix_root: shape too large");
-  if (iters_out) *iters_out = 0;
+  PTO_REQUIRE(n <= INT32_MAX && batch <= 65535 && max_iter <= INT32_MAX && max_iter * batch <= INT32_MAX,
+              "inverse_matrix_root: shape too large");
+  if (iters_out)
+    for (int64_t b = 0; b < (each ? batch : 1); ++b) iters_out[b] = 0;
   if (batch == 0 || n == 0) return 0;
   const int64_t ld = round_up(n, kPadK), sb = n * ld;
   const int nb = (int)batch;
@@ -252,8 +298,10 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   double* partial = cv.take<double>(kRedBlocks * batch);
   R* z = cv.take<R>(batch);
   R* xs = cv.take<R>(batch);
-  R* err = cv.take<R>(std::max<int64_t>(max_iter, 1));
-  RootState<R>* st = cv.take<RootState<R>>(1);
+  const int64_t n_err = std::max<int64_t>(max_iter, 1) * (each ? batch : 1);
+  const int64_t n_st = each ? 1 + batch : 1;
+  R* err = cv.take<R>(n_err);
+  RootState<R>* st = cv.take<RootState<R>>(n_st);
   R* buf[kRootBufs];
   for (int i = 0; i < kRootBufs; ++i) buf[i] = cv.take<R>(batch * sb);
   PTO_REQUIRE(!cv.overflow, "inverse_matrix_root: workspace too small");
@@ -284,27 +332,26 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   // Pads of the buffers written only by MFMA epilogues must read as zero.
   for (R* q : {X[1], Mi[1], Mk[1], tmp[0], tmp[1], tmp[2]})
     if (launch_zero_cols<R>(q, n, ld, n, sb, nb, stream)) return -1;
-  if (launch_fill<R>(err, std::max<int64_t>(max_iter, 1), R(0), stream)) return -1;
-  if (launch_fill<int>(reinterpret_cast<int*>(st), sizeof(RootState<R>) / sizeof(int), 0, stream)) return -1;
+  if (launch_fill<R>(err, n_err, R(0), stream)) return -1;
+  if (launch_fill<int>(reinterpret_cast<int*>(st), n_st * (int64_t)(sizeof(RootState<R>) / sizeof(int)), 0, stream))
+    return -1;
 
-  const int* guard = &st->stopped;
+  // GEMMs skip a stopped run: the one state, or matrix b's own
+  const int* guard = each ? &st[1].stopped : &st[0].stopped;
+  const int guard_stride = each ? (int)(sizeof(RootState<R>) / sizeof(int)) : 0;
   // dst = P·Q for symmetric Q (Q's rows are its columns); upper = the
   // product is symmetric too, computed on upper tiles and mirrored.
   auto product = [&](const R* P, const R* Q, R* dst, bool upper, const char* name) -> int {
-    GemmArgs g{P, ld, sb, Q, ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard};
+    GemmArgs g{P, ld, sb, Q, ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard, guard_stride};
     EpiStore<R, R> e{dst, ld, sb, vec_ok<R>(dst, ld, sb)};
-    if (upper) return launch_gemm<R, true>(g, e, nb, stream, name);
-    return launch_gemm<R, false>(g, e, nb, stream, name);
+    if (upper) return launch_gemm<R, true, EpiStore<R, R>, true>(g, e, nb, stream, name);
+    return launch_gemm<R, false, EpiStore<R, R>, true>(g, e, nb, stream, name);
   };
 
-  // X·Mi on upper tiles in fp64 only: in fp32 the full product, averaged by
-  // the final symmetrisation, ends the non-converging ill-conditioned runs
-  // (cond ~1e6) on a ~15% lower residual.
-  constexpr bool kSymX = sizeof(R) == 8;
   auto iteration = [&](int it) -> int {
     const int cur = it & 1, nxt = cur ^ 1;
     // X_{it+1} = X_it · Mi (symmetric: both are polynomials in M)
-    if (product(X[cur], Mi[cur], X[nxt], kSymX, "root_xmi")) return -1;
+    if (product(X[cur], Mi[cur], X[nxt], true, "root_xmi")) return -1;
     // S = Mi^p (torch.linalg.matrix_power order: direct for p <= 3, else
     // binary powering from the least significant bit)
     const R* S = nullptr;
@@ -350,12 +397,13 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     }
     // Mk_{it+1} = S · Mk_it, with the fused next-Mi / error epilogue.
     {
-      GemmArgs g{S, ld, sb, Mk[cur], ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard};
-      EpiMk<R> e{Mk[nxt], Mi[nxt], ld, sb, c1, alpha, reinterpret_cast<U*>(err + it), U(0),
-                    vec_ok<R>(Mk[nxt], ld, sb) && vec_ok<R>(Mi[nxt], ld, sb)};
-      if (launch_gemm<R, true>(g, e, nb, stream, "root_mk")) return -1;
+      GemmArgs g{S, ld, sb, Mk[cur], ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard, guard_stride};
+      EpiMk<R> e{Mk[nxt], Mi[nxt], ld, sb, c1, alpha, reinterpret_cast<U*>(err + (int64_t)it * (each ? nb : 1)),
+                 each ? 1 : 0, U(0), vec_ok<R>(Mk[nxt], ld, sb) && vec_ok<R>(Mi[nxt], ld, sb)};
+      if (launch_gemm<R, true, EpiMk<R>, true>(g, e, nb, stream, "root_mk")) return -1;
     }
-    hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(64), 0, stream, st, err, it, static_cast<R>(tol));
+    hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(each ? 256 : 64), 0, stream, st, err, it,
+                       static_cast<R>(tol), nb, (int)each);
     PTO_LAUNCHED("root_decide");
     return 0;
   };
@@ -374,18 +422,48 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   }
   {
     dim3 grid((unsigned)((n + 31) / 32), (unsigned)((n + 31) / 32), (unsigned)nb);
-    hipLaunchKernelGGL((root_final_kernel<R, TI>), grid, dim3(256), 0, stream, X[0], X[1], st, n, ld, sb, out);
+    hipLaunchKernelGGL((root_final_kernel<R, TI>), grid, dim3(256), 0, stream, X[0], X[1], st, (int)each, n, ld, sb,
+                       out);
     PTO_LAUNCHED("root_final");
   }
-  if (iters_out) *iters_out = host.iters;
+  if (iters_out && !each) *iters_out = host.iters;
+  if (iters_out && each) {
+    std::vector<RootState<R>> all((size_t)nb);
+    PTO_HIP(hipMemcpyAsync(all.data(), st + 1, sizeof(RootState<R>) * nb, hipMemcpyDeviceToHost, stream));
+    PTO_HIP(hipStreamSynchronize(stream));
+    for (int b = 0; b < nb; ++b) iters_out[b] = all[b].iters;
+  }
   return 0;
 }
 
 template <typename TI>
 int root_dispatch(const TI* A, TI* out, int root_f64, int64_t batch, int64_t n, int64_t p, double damping,
-                  int64_t max_iter, double tol, void* ws, size_t ws_bytes, int64_t* iters_out, hipStream_t s) {
-  if (root_f64) return root_t<TI, double>(A, out, batch, n, p, damping, max_iter, tol, ws, ws_bytes, iters_out, s);
-  return root_t<TI, float>(A, out, batch, n, p, damping, max_iter, tol, ws, ws_bytes, iters_out, s);
+                  int64_t max_iter, double tol, bool each, void* ws, size_t ws_bytes, int64_t* iters_out,
+                  hipStream_t s) {
+  if (root_f64)
+    return root_t<TI, double>(A, out, batch, n, p, damping, max_iter, tol, each, ws, ws_bytes, iters_out, s);
+  return root_t<TI, float>(A, out, batch, n, p, damping, max_iter, tol, each, ws, ws_bytes, iters_out, s);
+}
+
+int root_entry(const void* A, void* out, int dtype, int root_f64, int64_t batch, int64_t n, int64_t p,
+               double damping, int64_t max_iter, double tol, bool each, void* workspace, size_t ws_bytes,
+               int64_t* iters_out, void* stream) {
+  PTO_REQUIRE(batch >= 0 && n >= 0 && max_iter >= 0, "inverse_matrix_root: negative extent or max_iter");
+  PTO_REQUIRE(batch * n == 0 || (A && out && workspace), "inverse_matrix_root: null input, output or workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case kF32:
+      return root_dispatch<float>(static_cast<const float*>(A), static_cast<float*>(out), root_f64, batch, n, p,
+                                  damping, max_iter, tol, each, workspace, ws_bytes, iters_out, s);
+    case kF64:
+      return root_dispatch<double>(static_cast<const double*>(A), static_cast<double*>(out), root_f64, batch, n, p,
+                                   damping, max_iter, tol, each, workspace, ws_bytes, iters_out, s);
+    case kBF16:
+      return root_dispatch<bf16>(static_cast<const bf16*>(A), static_cast<bf16*>(out), root_f64, batch, n, p,
+                                 damping, max_iter, tol, each, workspace, ws_bytes, iters_out, s);
+    default:
+      PTO_REQUIRE(false, "inverse_matrix_root: unsupported dtype code");
+  }
 }
 
 }  // namespace
@@ -394,28 +472,27 @@ int root_dispatch(const TI* A, TI* out, int root_f64, int64_t batch, int64_t n, 
 extern "C" {
 
 size_t pto_inverse_root_workspace_bytes(int root_f64, int64_t batch, int64_t n, int64_t max_iter) {
-  return root_f64 ? pto::root_ws_bytes_t<double>(batch, n, max_iter) : pto::root_ws_bytes_t<float>(batch, n, max_iter);
+  return root_f64 ? pto::root_ws_bytes_t<double>(batch, n, max_iter, false)
+                  : pto::root_ws_bytes_t<float>(batch, n, max_iter, false);
 }
 
 int pto_inverse_root(const void* A, void* out, int dtype, int root_f64, int64_t batch, int64_t n, int64_t p,
                      double damping, int64_t max_iter, double tol, void* workspace, size_t ws_bytes,
                      int64_t* iters_out, void* stream) {
-  PTO_REQUIRE(batch >= 0 && n >= 0 && max_iter >= 0, "inverse_matrix_root: negative extent or max_iter");
-  PTO_REQUIRE(batch * n == 0 || (A && out && workspace), "inverse_matrix_root: null input, output or workspace");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case pto::kF32:
-      return pto::root_dispatch<float>(static_cast<const float*>(A), static_cast<float*>(out), root_f64, batch, n, p,
-                                       damping, max_iter, tol, workspace, ws_bytes, iters_out, s);
-    case pto::kF64:
-      return pto::root_dispatch<double>(static_cast<const double*>(A), static_cast<double*>(out), root_f64, batch, n,
-                                        p, damping, max_iter, tol, workspace, ws_bytes, iters_out, s);
-    case pto::kBF16:
-      return pto::root_dispatch<pto::bf16>(static_cast<const pto::bf16*>(A), static_cast<pto::bf16*>(out), root_f64,
-                                           batch, n, p, damping, max_iter, tol, workspace, ws_bytes, iters_out, s);
-    default:
-      PTO_REQUIRE(false, "inverse_matrix_root: unsupported dtype code");
-  }
+  return pto::root_entry(A, out, dtype, root_f64, batch, n, p, damping, max_iter, tol, false, workspace, ws_bytes,
+                         iters_out, stream);
+}
+
+size_t pto_inverse_root_each_workspace_bytes(int root_f64, int64_t batch, int64_t n, int64_t max_iter) {
+  return root_f64 ? pto::root_ws_bytes_t<double>(batch, n, max_iter, true)
+                  : pto::root_ws_bytes_t<float>(batch, n, max_iter, true);
+}
+
+int pto_inverse_root_each(const void* A, void* out, int dtype, int root_f64, int64_t batch, int64_t n, int64_t p,
+                          double damping, int64_t max_iter, double tol, void* workspace, size_t ws_bytes,
+                          int64_t* iters_out, void* stream) {
+  return pto::root_entry(A, out, dtype, root_f64, batch, n, p, damping, max_iter, tol, true, workspace, ws_bytes,
+                         iters_out, stream);
 }
 
 }  // extern "C"

@@ -11,8 +11,10 @@ Backends (the same switch as the reference's pytorch_opt/ops/__init__.py:16-88):
 raises (it warns and returns False). ``PYTORCH_OPT_NATIVE=1`` at import
 calls it. Op signatures and defaults are the reference's
 (pytorch_opt/ops/__init__.py:58-84); ``gram_update_`` (K-FAC factor
-statistics), ``two_sided_product`` (SOAP's rotations) and ``adamw_step_``
-(the optimizers' shared AdamW fallback) are additive.
+statistics), ``two_sided_product`` (SOAP's rotations), ``adamw_step_``
+(the optimizers' shared AdamW fallback) and ``inverse_matrix_root_each``
+(one root per matrix of a stack, the optimizers' per-factor calls) are
+additive.
 """
 
 from __future__ import annotations
@@ -77,6 +79,21 @@ def inverse_matrix_root(A, p, damping=0.0, method="auto", root_dtype=torch.float
                                          root_dtype=root_dtype, max_iter=max_iter, tol=tol)
 
 
+def inverse_matrix_root_each(A, p, damping=0.0, method="auto", root_dtype=torch.float64, max_iter=100, tol=1e-10):
+    """inverse_matrix_root of each matrix of a stack A [k, n, n] on its own,
+    i.e. the k separate calls the reference's optimizers make (each with its
+    own Newton stop rule), as one call: the HIP backend runs the coupled
+    Newton iterations of the whole stack in one launch sequence."""
+    if A.dim() != 3:
+        raise OpsArgumentError(f"inverse_matrix_root_each expects [k, n, n], got {tuple(A.shape)}")
+    if _use_native() and A.is_cuda and _NATIVE.newton_for(method):
+        out, _ = _NATIVE.inverse_matrix_root_each(A, int(p), float(damping), root_dtype == torch.float64,
+                                                  int(max_iter), float(tol))
+        return out
+    return torch.stack([inverse_matrix_root(a, p, damping=damping, method=method, root_dtype=root_dtype,
+                                            max_iter=max_iter, tol=tol) for a in A])
+
+
 def newton_schulz_orthogonalize(G, steps=5, coeffs=(3.4445, -4.7750, 2.0315), eps=1e-7):
     if _use_native():
         a, b, c = coeffs
@@ -124,6 +141,7 @@ def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
 
 
 __all__ = ["get_backend", "set_backend", "native_available", "load_native", "inverse_matrix_root",
+           "inverse_matrix_root_each",
            "newton_schulz_orthogonalize", "kron_factor_update_", "precond_apply_two_sided",
            "two_sided_product", "gram_update_", "adamw_step_", "OpsArgumentError", "reference"]
 

@@ -22,6 +22,10 @@ from .reference import OpsArgumentError, ROOT_METHODS
 
 _DTYPE_CODE = {torch.float32: 0, torch.float64: 1, torch.bfloat16: 2}
 
+# Root methods that run the coupled Newton kernels on GPU tensors; "eigh"
+# stays on torch.linalg.eigh (an eigendecomposition, not one of the kernels).
+_NEWTON_METHODS = ("auto", "newton")
+
 _c_size = ctypes.c_size_t
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -45,6 +49,9 @@ SIGNATURES = {
     "pto_inverse_root_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
     "pto_inverse_root": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_dbl, _c_i64,
                                   _c_dbl, _c_ptr, _c_size, ctypes.POINTER(_c_i64), _c_ptr]),
+    "pto_inverse_root_each_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "pto_inverse_root_each": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_dbl, _c_i64,
+                                       _c_dbl, _c_ptr, _c_size, ctypes.POINTER(_c_i64), _c_ptr]),
     "pto_precond_apply_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
     "pto_precond_apply": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_ptr, _c_size,
                                    _c_ptr]),
@@ -154,6 +161,11 @@ class HipBackend:
         if Rw is not R:
             R.copy_(Rw)
 
+    @staticmethod
+    def newton_for(method: str) -> bool:
+        """Whether `method` runs the coupled Newton kernels on GPU tensors."""
+        return method in _NEWTON_METHODS
+
     def inverse_matrix_root(self, A, p, damping, method, root_f64, max_iter, tol):
         return self.inverse_matrix_root_iters(A, p, damping, method, root_f64, max_iter, tol)[0]
 
@@ -164,7 +176,7 @@ class HipBackend:
         if method not in ROOT_METHODS:
             raise OpsArgumentError(f"method must be one of {ROOT_METHODS}, got {method!r}")
         root_dtype = torch.float64 if root_f64 else torch.float32
-        if not A.is_cuda or method == "eigh":
+        if not A.is_cuda or not self.newton_for(method):
             # eigendecomposition is not one of the kernels here: torch's eigh
             return reference.inverse_matrix_root_with_iters(A, p, damping, method, root_dtype, max_iter, tol)
         if A.dim() < 2 or A.shape[-1] != A.shape[-2]:
@@ -186,6 +198,37 @@ class HipBackend:
                                             ctypes.byref(iters), self._stream(Ac.device))
         self._check(rc, "inverse_matrix_root")
         return out, int(iters.value)
+
+    def inverse_matrix_root_each(self, A, p, damping, root_f64, max_iter, tol):
+        """Coupled-Newton roots of a stack A [k, n, n] of independent matrices,
+        each by its own stop rule (what k separate inverse_matrix_root calls
+        return), in one launch sequence. Returns (roots, iterations per matrix)."""
+        if int(p) != p or p < 1:
+            raise OpsArgumentError(f"p must be a positive integer, got {p}")
+        if A.dim() != 3 or A.shape[-1] != A.shape[-2]:
+            raise OpsArgumentError(f"inverse_matrix_root_each expects [k, n, n], got {tuple(A.shape)}")
+        if not A.is_cuda:
+            outs = [reference.inverse_matrix_root_with_iters(a, p, damping, "newton",
+                                                             torch.float64 if root_f64 else torch.float32,
+                                                             max_iter, tol) for a in A]
+            return torch.stack([o for o, _ in outs]), [i for _, i in outs]
+        if A.dtype not in _DTYPE_CODE:
+            out, iters = self.inverse_matrix_root_each(A.float(), p, damping, root_f64, max_iter, tol)
+            return out.to(A.dtype), iters
+        Ac = A.contiguous()
+        k, n = Ac.shape[0], Ac.shape[-1]
+        out = torch.empty_like(Ac)
+        code = _DTYPE_CODE[Ac.dtype]
+        iters = (_c_i64 * max(k, 1))()
+        with torch.cuda.device(Ac.device):
+            nbytes = self._lib.pto_inverse_root_each_workspace_bytes(int(bool(root_f64)), k, n,
+                                                                     max(int(max_iter), 0))
+            ws = self._workspace(nbytes, Ac.device)
+            rc = self._lib.pto_inverse_root_each(_ptr(Ac), _ptr(out), code, int(bool(root_f64)), k, n, int(p),
+                                                 float(damping), max(int(max_iter), 0), float(tol), _ptr(ws),
+                                                 nbytes, iters, self._stream(Ac.device))
+        self._check(rc, "inverse_matrix_root_each")
+        return out, [int(iters[i]) for i in range(k)]
 
     def precond_apply_two_sided(self, L_root, G, R_root):
         if not (L_root.is_cuda and G.is_cuda and R_root.is_cuda):

@@ -51,7 +51,8 @@ def _top_eigenvalues(M: torch.Tensor, iters: int) -> torch.Tensor:
 def damped_inverses_newton(mats, gammas, batch_bytes: int = 4 << 30, power_iters: int = 30):
     """(F_i + γ_i·I)⁻¹ for each factor by the coupled Newton iteration of
     ops.inverse_matrix_root with p = 1 (the MFMA root kernels on a GPU),
-    same-shape factors in one batched call, in the factor's precision
+    same-shape factors in one ops.inverse_matrix_root_each call (each with
+    its own stop rule), in the factor's precision
     (float64 factors in float64, others in float32). Also returns the
     condition number of each F_i + γ_i·I estimated as λ_max(F + γI)·λ_max
     of the inverse, both by power iteration. Returns [(inverse, cond)]."""
@@ -69,8 +70,8 @@ def damped_inverses_newton(mats, gammas, batch_bytes: int = 4 << 30, power_iters
         for s in range(0, len(idx), step):
             chunk = idx[s:s + step]
             M = torch.stack([mats[i].to(rdt) + gammas[i] * eye for i in chunk])
-            inv = ops.inverse_matrix_root(M, 1, damping=0.0, method="newton", root_dtype=rdt,
-                                          tol=1e-10 if rdt == torch.float64 else 1e-5)
+            inv = ops.inverse_matrix_root_each(M, 1, damping=0.0, method="newton", root_dtype=rdt,
+                                               tol=1e-10 if rdt == torch.float64 else 1e-5)
             cond = (_top_eigenvalues(M, power_iters) * _top_eigenvalues(inv, power_iters)).tolist()
             for j, i in enumerate(chunk):
                 out[i] = (inv[j].to(dt), cond[j])

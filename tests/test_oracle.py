@@ -189,6 +189,70 @@ def test_coupled_newton_iteration_count_pinned_in_float64(p):
     assert n_wide > n_scalar
 
 
+def _config4_input(n):
+    """The ill-conditioned config-4 construction (tests/golden/config4_roots.py)
+    at a small size: float32 Q·diag(λ)·Qᵀ, λ = 10^U(−6, 0)."""
+    from golden.config4_roots import build_input
+
+    return build_input(n).numpy()
+
+
+def _k_split(parts):
+    """Matrix product whose contraction is summed in `parts` float32 partial sums."""
+
+    def mm(a, b):
+        k = a.shape[-1]
+        out = None
+        for q in range(parts):
+            lo, hi = q * k // parts, (q + 1) * k // parts
+            t = a[..., :, lo:hi] @ b[..., lo:hi, :]
+            out = t if out is None else out + t
+        return out
+
+    return mm
+
+
+def test_coupled_newton_fp32_residual_moves_with_summation_order():
+    """At cond ~5e5 the float32 coupled Newton never reaches tol; its returned
+    iterate, and so the residual ‖X⁴(A+εI) − I‖_F/√n, is set by product
+    rounding. Summing each product's contraction in two or four partial sums
+    (a legal reordering) moves the oracle's own residual by far more than
+    1e-3, so two float32 implementations are compared one-sided: a kernel's
+    residual may not exceed the oracle's by more than 1e-3."""
+    A = _config4_input(256)
+    resid = {}
+    for parts in (1, 2, 4):
+        X, it = oo.inverse_root(A, 4, damping=1e-6, method="newton", root_dtype=np.float32, max_iter=40,
+                                matmul=_k_split(parts))
+        assert it == 40  # the float32 error floor sits far above tol = 1e-10
+        resid[parts] = float(oo.root_residual(X, A, 4, 1e-6))
+    assert abs(resid[1] - resid[2]) > 3e-3 and abs(resid[1] - resid[4]) > 3e-3, resid
+    # the same iteration in float64 meets tol; its root, stored in the input's
+    # float32, sits at that storage rounding (~2e-4), far below all three
+    X64, it64 = oo.inverse_root(A, 4, damping=1e-6, method="newton", root_dtype=np.float64)
+    assert it64 < 40 and oo.root_residual(X64, A, 4, 1e-6) < 1e-3 < min(resid.values()) / 5
+
+
+def test_config4_golden_residual_reproduces():
+    """The committed config-4 golden values come from this oracle on this
+    input: re-run the n = 1024 case (about 5 s) and compare."""
+    import json
+    import os
+
+    from golden import config4_roots as c4
+
+    with open(c4.GOLDEN) as f:
+        gold = json.load(f)
+    case = gold["cases"]["1024"]
+    A = c4.build_input(1024)
+    np.testing.assert_allclose(c4.checksum(A), case["input_checksum"], rtol=1e-9)
+    X, it = oo.inverse_root(A.numpy(), c4.P, damping=c4.EPS, method="newton", root_dtype=np.float32,
+                            max_iter=c4.MAX_ITER, tol=c4.TOL)
+    assert it == case["iterations"]
+    assert abs(float(oo.root_residual(X, A.numpy(), c4.P, c4.EPS)) - case["residual"]) < 1e-9
+    assert os.path.basename(c4.GOLDEN) == "root_config4.json"
+
+
 def test_newton_matches_eigh_and_damping():
     # the reference's tests/test_ops_reference.py:24-38
     A, _, _ = _spd(8, 3)
