@@ -57,6 +57,22 @@ int pto_ns5(const void* G, void* out, int dtype, int64_t batch, int64_t rows, in
             double a, double b, double c, double eps, void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * pto_ns5 without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). It has no counterpart in the
+ * reference. The workspace is a static 256 MiB device array in the library,
+ * one per GPU, allocated when the library's code is loaded on that GPU and
+ * held until the process ends; a call whose pto_ns5_workspace_bytes exceeds
+ * 256 MiB fails before any launch (bf16 up to one 4096x11008 matrix, fp32
+ * up to 2048x8192). The call itself allocates nothing: no hipMalloc, no
+ * events (kernel timing is off for it). Every call on a GPU shares that
+ * GPU's array, so calls that overlap on one GPU (other streams, other
+ * threads) race; serialise them. G, out and the result are as for pto_ns5.
+ */
+int pto_ns5_noalloc(const void* G, void* out, int dtype, int64_t batch, int64_t rows, int64_t cols, int64_t steps,
+                    double a, double b, double c, double eps, void* stream);
+
+/*
  * In-place Kronecker factor update. Replaces
  *   _NATIVE.kron_factor_update_(L, R, G, beta2)
  * called at pytorch_opt/ops/__init__.py:76; semantics of

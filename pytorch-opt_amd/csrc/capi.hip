@@ -70,7 +70,11 @@ int drain(ProfState& p) {
 
 }  // namespace
 
-bool prof_enabled() { return prof().enabled; }
+static thread_local int g_prof_suspended = 0;
+
+bool prof_enabled() { return g_prof_suspended == 0 && prof().enabled; }
+
+void prof_suspend(int delta) { g_prof_suspended += delta; }
 
 void prof_begin(const char* name, hipStream_t stream, void** token) {
   ProfState& p = prof();

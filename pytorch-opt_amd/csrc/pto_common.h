@@ -80,9 +80,17 @@ struct Carver {
 };
 
 // Per-launch profiling hooks (HIP events around selected launches).
-bool prof_enabled();
+bool prof_enabled();  // false on a thread inside a ProfSuspend scope
+void prof_suspend(int delta);
 void prof_begin(const char* name, hipStream_t stream, void** token);
 void prof_end(void* token, hipStream_t stream);
+
+// Keeps kernel timing off on this thread for the scope (the timing creates
+// events, which a caller that may not allocate cannot have).
+struct ProfSuspend {
+  ProfSuspend() { prof_suspend(1); }
+  ~ProfSuspend() { prof_suspend(-1); }
+};
 
 struct ProfScope {
   void* tok = nullptr;

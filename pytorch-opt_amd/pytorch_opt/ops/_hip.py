@@ -40,6 +40,8 @@ SIGNATURES = {
     "pto_ns5_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
     "pto_ns5": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_dbl, _c_dbl, _c_dbl,
                          _c_dbl, _c_ptr, _c_size, _c_ptr]),
+    "pto_ns5_noalloc": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_dbl, _c_dbl, _c_dbl,
+                                 _c_dbl, _c_ptr]),
     "pto_kron_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64]),
     "pto_kron_factor_update": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_dbl, _c_ptr,
                                         _c_size, _c_ptr]),
@@ -129,6 +131,25 @@ class HipBackend:
                                    float(a), float(b), float(c), float(eps), _ptr(ws), nbytes,
                                    self._stream(Gc.device))
         self._check(rc, "newton_schulz_orthogonalize")
+        return out
+
+    def newton_schulz_orthogonalize_into(self, G, out, steps, a, b, c, eps):
+        """NS5 of a contiguous GPU tensor G into the caller's `out` (same shape
+        and dtype) through pto_ns5_noalloc: nothing is allocated, the library's
+        static per-GPU scratch serves as the workspace."""
+        if G.dim() < 2:
+            raise OpsArgumentError("newton_schulz_orthogonalize expects a matrix (ndim >= 2)")
+        if not (G.is_cuda and out.is_cuda and G.is_contiguous() and out.is_contiguous()):
+            raise OpsArgumentError("newton_schulz_orthogonalize_into: contiguous GPU tensors only")
+        if out.shape != G.shape or out.dtype != G.dtype or G.dtype not in _DTYPE_CODE:
+            raise OpsArgumentError("newton_schulz_orthogonalize_into: out must match G (float32, float64, bfloat16)")
+        rows, cols = G.shape[-2], G.shape[-1]
+        batch = math.prod(G.shape[:-2])
+        with torch.cuda.device(G.device):
+            rc = self._lib.pto_ns5_noalloc(_ptr(G), _ptr(out), _DTYPE_CODE[G.dtype], batch, rows, cols,
+                                           max(int(steps), 0), float(a), float(b), float(c), float(eps),
+                                           self._stream(G.device))
+        self._check(rc, "newton_schulz_orthogonalize_into")
         return out
 
     def kron_factor_update_(self, L, R, G, beta2):

@@ -1,0 +1,40 @@
+"""The entry point that allocates nothing (pto_ns5_noalloc) against pto_ns5
+on the same inputs: bit-identical outputs on two calls in a row, the second
+smaller (the shared static scratch keeps the first call's contents), and a
+call too large for the scratch refused before any launch."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+COEFFS = (3.4445, -4.7750, 2.0315)
+
+
+def _input(shape, dtype, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (1e-3 * torch.randn(shape, generator=g, device=DEV)).to(dtype)
+
+
+@pytest.mark.parametrize("dtype, big, small", [
+    (torch.bfloat16, (4096, 4096), (384, 1000)),
+    (torch.float32, (2, 1024, 2304), (300, 70)),
+])
+def test_noalloc_matches_ns5_twice(hip, dtype, big, small):
+    a, b, c = COEFFS
+    for i, shape in enumerate((big, small)):
+        G = _input(shape, dtype, 100 + i)
+        want = hip.newton_schulz_orthogonalize(G, 5, a, b, c, 1e-7)
+        out = torch.full_like(G, float("nan"))
+        torch.cuda.synchronize()
+        hip.newton_schulz_orthogonalize_into(G, out, 5, a, b, c, 1e-7)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), (dtype, shape)
+
+
+def test_noalloc_rejects_oversize_call(hip):
+    G = torch.empty(4096, 4096, device=DEV)  # fp32 4096² needs 320 MiB of workspace
+    out = torch.empty_like(G)
+    with pytest.raises(RuntimeError, match="bytes of scratch"):
+        hip.newton_schulz_orthogonalize_into(G, out, 5, *COEFFS, 1e-7)
