@@ -1,15 +1,18 @@
-"""EKFAC (George et al.): K-FAC's Kronecker eigenbasis with a rescaled diagonal.
+"""EKFAC (George et al.): K-FAC's Kronecker eigenbasis with a rescaled
+diagonal.
 
-Same behaviour as the reference's pytorch_opt/optim/ekfac.py: every
-``inv_every`` steps the float64 eigenbases Q_A, Q_G of the factors (and their
-eigenvalues, for the condition diagnostics) are refreshed (:27-42); each
-step the rotated gradient Vt = Q_Gᵀ·V·Q_A updates per-entry second moments
-s (initialised to Vt², then an EMA with ``scale_decay``) and the direction
-is Q_G·(Vt / (s + damping))·Q_Aᵀ (:44-58). With s fixed to the outer
-product of the factor eigenvalues and no damping this is K-FAC.
+Behaviour of the reference's pytorch_opt/optim/ekfac.py: every
+``inv_every`` steps the float64 eigenbases Q_A, Q_G of the factors are
+refreshed (:27-42); each step the rotated gradient Vt = Q_Gᵀ·V·Q_A updates
+per-entry second moments s (Vt² the first time, then an EMA with
+``scale_decay``, kept across refreshes) and the direction is
+Q_G·(Vt / (s + damping))·Q_Aᵀ (:44-58). With s fixed to the outer product of
+the factors' eigenvalues and no damping this is K-FAC's direction.
 
-The two rotations are ops.two_sided_product calls (MFMA kernels on a GPU);
-the refresh eighs of same-shape factors share one batched call.
+Here both rotations are ops.two_sided_product calls (MFMA kernels on a GPU),
+the refresh eighs of same-shape factors share one batched call, and the
+scales live in each module's curvature entry (so they travel with the
+K-FAC checkpoint state).
 """
 
 from __future__ import annotations
@@ -20,56 +23,55 @@ from .. import ops
 from .kfac import KFAC, batched_eigh
 
 
+def _cond(ev: torch.Tensor, lam: float) -> float:
+    return float(ev.max() + lam) / max(float(ev.min()) + lam, 1e-300)
+
+
 class EKFAC(KFAC):
     def __init__(self, model, *args, scale_decay: float = 0.95, **kwargs):
         if kwargs.get("inverse_method", "eigh") != "eigh":
             raise ValueError("EKFAC preconditions in the factors' eigenbases: inverse_method must be 'eigh'")
-        self._scales: dict[str, torch.Tensor] = {}
-        self._scale_decay = scale_decay
+        self.scale_decay = scale_decay
         super().__init__(model, *args, **kwargs)
 
     def _refresh_inverses(self):
         lam = self.param_groups[0]["damping"]
         names = list(self.tracker.factors)
-        facs = [self.tracker.factors[n] for n in names]
-        eig = batched_eigh([F for f in facs for F in (f["A"], f["G"])])
+        flat = [self.tracker.factors[n][k] for n in names for k in ("A", "G")]
+        eig = batched_eigh(flat)
         conds = []
-        for i, (name, f) in enumerate(zip(names, facs)):
-            (evA, QA), (evG, QG) = eig[2 * i], eig[2 * i + 1]
-            dt = f["A"].dtype
-            cA = float((evA.max() + lam) / max(float(evA.min()) + lam, 1e-300))
-            cG = float((evG.max() + lam) / max(float(evG.min()) + lam, 1e-300))
-            self._inv[name] = {"QA": QA.to(dt), "QG": QG.to(dt), "evA": evA.to(dt), "evG": evG.to(dt),
-                               "cond_A": cA, "cond_G": cG}
-            conds.append((cA, cG))
+        for k, name in enumerate(names):
+            (evA, QA), (evG, QG) = eig[2 * k], eig[2 * k + 1]
+            dt = flat[2 * k].dtype
+            entry = {"QA": QA.to(dt), "QG": QG.to(dt), "evA": evA.to(dt), "evG": evG.to(dt),
+                     "cond_A": _cond(evA, lam), "cond_G": _cond(evG, lam)}
+            previous = self._inv.get(name, {})
+            if "scale" in previous:  # the second moments outlive the basis
+                entry["scale"] = previous["scale"]
+            self._inv[name] = entry
+            conds.append((entry["cond_A"], entry["cond_G"]))
         return conds
 
     def _precondition(self, name: str, V: torch.Tensor) -> torch.Tensor:
         inv = self._inv.get(name)
         if inv is None:
             raise RuntimeError(f"Missing EKFAC inverse for {name!r}")
-        dtype = V.dtype
-        V = V.to(inv["QG"].dtype)
-        lam = self.param_groups[0]["damping"]
-        Vt = ops.two_sided_product(inv["QG"], V, inv["QA"], transpose_a=True)
-        s = self._scales.get(name)
-        if s is None:
-            s = Vt.pow(2).detach().clone()
-            self._scales[name] = s
+        QG, QA = inv["QG"], inv["QA"]
+        Vt = ops.two_sided_product(QG, V.to(QG.dtype), QA, transpose_a=True)
+        moment = Vt.square()
+        scale = inv.get("scale")
+        if scale is None:
+            scale = inv["scale"] = moment
         else:
-            s.mul_(self._scale_decay).add_(Vt.pow(2), alpha=1 - self._scale_decay)
-        return ops.two_sided_product(inv["QG"], Vt / (s + lam), inv["QA"], transpose_b=True).to(dtype)
+            scale.mul_(self.scale_decay).add_(moment, alpha=1.0 - self.scale_decay)
+        lam = self.param_groups[0]["damping"]
+        return ops.two_sided_product(QG, Vt / (scale + lam), QA, transpose_b=True).to(V.dtype)
 
-    def state_dict(self):
-        sd = super().state_dict()
-        sd["ekfac"] = {"scales": dict(self._scales), "scale_decay": self._scale_decay}
-        return sd
+    def _extra_state(self) -> dict:
+        state = super()._extra_state()
+        state["scale_decay"] = self.scale_decay
+        return state
 
-    def load_state_dict(self, sd):
-        sd = dict(sd)
-        extra = sd.pop("ekfac", None)
-        super().load_state_dict(sd)
-        if extra is not None:
-            self._scale_decay = extra.get("scale_decay", self._scale_decay)
-            restored = self._restore_curvature({n: {"scale": v} for n, v in extra["scales"].items()})
-            self._scales = {n: d["scale"] for n, d in restored.items()}
+    def load_state_dict(self, state_dict):
+        self.scale_decay = state_dict.get("kfac", {}).get("scale_decay", self.scale_decay)
+        super().load_state_dict(state_dict)

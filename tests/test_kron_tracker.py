@@ -1,10 +1,20 @@
-"""KronTracker factors routed through ops.gram_update_: the reference's
-hand-computed factors, EMA vs running mean, Conv2d 1x1 == Linear and the
-autocast precision tests (tests/test_kron_tracker.py:9-53,142-147 of the
-reference), on CPU and, on a GPU box, through the HIP Gram kernel."""
+"""KronTracker (factor statistics through ops.gram_update_) against brute
+force, on CPU and, on a GPU box, through the HIP Gram kernel:
+
+* A and G of a Linear layer equal sums of per-row outer products;
+* the blend schedule over three batches (EMA weights β², β(1−β), 1−β; the
+  running mean 1/3 each);
+* a module called twice in one forward contributes both calls, each
+  activation paired with its own output gradient;
+* a padded, strided 3x3 convolution's factors equal those of its explicit
+  unfolded patches;
+* the loss scale divides out of G, capture gates the forward binding, and
+  bf16 activations keep float32 factors.
+"""
 
 import pytest
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from pytorch_opt import KronTracker, ops
@@ -19,92 +29,118 @@ def _backend(device):
     ops.set_backend("auto")
 
 
-def mse_half(pred, target):
-    return 0.5 * (pred - target).pow(2).sum() / pred.shape[0]
+def _outer_sum(rows):
+    return sum(torch.outer(r, r) for r in rows)
 
 
-def test_linear_factors_hand_computed(device):
-    torch.manual_seed(1)
-    lin = nn.Linear(3, 2).to(device)
-    X = torch.randn(4, 3, device=device)
-    y = torch.randn(4, 2, device=device)
+def test_linear_factors_are_outer_product_sums(device):
+    gen = torch.Generator().manual_seed(11)
+    lin = nn.Linear(5, 3).double().to(device)
+    X = torch.randn(7, 5, generator=gen, dtype=torch.float64).to(device)
     tr = KronTracker(lin)
     with tr.track():
         out = lin(X)
-        mse_half(out, y).backward()
-    a_aug = torch.cat([X, X.new_ones(4, 1)], dim=1)
-    ghat = out.detach() - y  # B · dL/dout for mse_half
-    assert torch.allclose(tr.factors[""]["A"], a_aug.T @ a_aug / 4, atol=1e-6)
-    assert torch.allclose(tr.factors[""]["G"], ghat.T @ ghat / 4, atol=1e-6)
+        out.retain_grad()
+        (out.pow(3).sum() / 7).backward()  # a mean-reduced loss
+    n = 7
+    a_rows = torch.cat([X, torch.ones(n, 1, dtype=X.dtype, device=device)], 1)
+    g_rows = n * out.grad  # per-example output gradients
+    torch.testing.assert_close(tr.factors[""]["A"], _outer_sum(a_rows) / n, rtol=1e-12, atol=1e-14)
+    torch.testing.assert_close(tr.factors[""]["G"], _outer_sum(g_rows) / n, rtol=1e-12, atol=1e-14)
+    assert tr.updates("") == 1
 
 
-def _one_pass(lin, X, y, tr):
+@pytest.mark.parametrize("decay", [0.8, None])
+def test_three_batch_blend(device, decay):
+    gen = torch.Generator().manual_seed(12)
+    lin = nn.Linear(4, 2, bias=False).to(device)
+    tr = KronTracker(lin, ema_decay=decay)
+    batches = [torch.randn(6, 4, generator=gen).to(device) for _ in range(3)]
+    for X in batches:
+        with tr.track():
+            torch.autograd.grad(lin(X).square().mean(), [lin.weight])
+    grams = [X.T @ X / 6 for X in batches]
+    w = [decay * decay, decay * (1 - decay), 1 - decay] if decay is not None else [1 / 3] * 3
+    torch.testing.assert_close(tr.factors[""]["A"], sum(wi * Gi for wi, Gi in zip(w, grams)), rtol=1e-5, atol=1e-6)
+    assert tr.updates("") == 3
+
+
+def test_reused_module_pairs_each_call(device):
+    """x -> lin -> tanh -> lin: two calls per forward, each bound to its own
+    input, so A is the running mean of the two calls' activation Grams."""
+    gen = torch.Generator().manual_seed(13)
+    lin = nn.Linear(6, 6, bias=False).double().to(device)
+    X = torch.randn(9, 6, generator=gen, dtype=torch.float64).to(device)
+    tr = KronTracker(lin, ema_decay=None)
     with tr.track():
-        return torch.autograd.grad(mse_half(lin(X), y), list(lin.parameters()))
+        h = torch.tanh(lin(X))
+        lin(h).sum().backward()
+    want = 0.5 * (X.T @ X / 9 + h.detach().T @ h.detach() / 9)
+    torch.testing.assert_close(tr.factors[""]["A"], want, rtol=1e-12, atol=1e-14)
+    assert tr.updates("") == 2
 
 
-def test_ema_vs_running_mean(device):
-    torch.manual_seed(2)
-    lin = nn.Linear(3, 2, bias=False).to(device)
-    X1, y1 = torch.randn(4, 3, device=device), torch.randn(4, 2, device=device)
-    X2, y2 = torch.randn(4, 3, device=device), torch.randn(4, 2, device=device)
-    ema = KronTracker(lin, ema_decay=0.9)
-    _one_pass(lin, X1, y1, ema)
-    _one_pass(lin, X2, y2, ema)
-    assert torch.allclose(ema.factors[""]["A"], 0.9 * X1.T @ X1 / 4 + 0.1 * X2.T @ X2 / 4, atol=1e-6)
-    ema.remove()
-    rm = KronTracker(lin, ema_decay=None)
-    _one_pass(lin, X1, y1, rm)
-    _one_pass(lin, X2, y2, rm)
-    assert torch.allclose(rm.factors[""]["A"], 0.5 * (X1.T @ X1 / 4 + X2.T @ X2 / 4), atol=1e-6)
+def test_conv_factors_are_unfolded_patch_grams(device):
+    gen = torch.Generator().manual_seed(14)
+    conv = nn.Conv2d(3, 4, kernel_size=3, stride=2, padding=1).double().to(device)
+    X = torch.randn(2, 3, 7, 7, generator=gen, dtype=torch.float64).to(device)
+    tr = KronTracker(conv)
+    with tr.track():
+        out = conv(X)
+        out.retain_grad()
+        (out.square().sum() / 2).backward()
+    B, L = 2, out.shape[-1] * out.shape[-2]
+    patches = F.unfold(X, 3, padding=1, stride=2).transpose(1, 2).reshape(B * L, -1)
+    a_rows = torch.cat([patches, torch.ones(B * L, 1, dtype=X.dtype, device=device)], 1)
+    g_rows = B * out.grad.flatten(2).transpose(1, 2).reshape(B * L, -1)
+    torch.testing.assert_close(tr.factors[""]["A"], a_rows.T @ a_rows / (B * L), rtol=1e-12, atol=1e-13)
+    torch.testing.assert_close(tr.factors[""]["G"], g_rows.T @ g_rows / (B * L), rtol=1e-12, atol=1e-13)
 
 
-def test_conv_1x1_output_equals_linear(device):
-    torch.manual_seed(3)
-    conv = nn.Conv2d(2, 5, kernel_size=4).to(device)
-    lin = nn.Linear(32, 5).to(device)
-    with torch.no_grad():
-        lin.weight.copy_(conv.weight.reshape(5, -1))
-        lin.bias.copy_(conv.bias)
-    X = torch.randn(3, 2, 4, 4, device=device)
-    y = torch.randn(3, 5, device=device)
-    tc, tl = KronTracker(conv), KronTracker(lin)
-    with tc.track():
-        torch.autograd.grad(mse_half(conv(X).reshape(3, 5), y), list(conv.parameters()))
-    with tl.track():
-        torch.autograd.grad(mse_half(lin(X.reshape(3, -1)), y), list(lin.parameters()))
-    assert torch.allclose(tc.factors[""]["A"], tl.factors[""]["A"], atol=1e-5)
-    assert torch.allclose(tc.factors[""]["G"], tl.factors[""]["G"], atol=1e-5)
+def test_loss_scale_divides_out(device):
+    gen = torch.Generator().manual_seed(15)
+    lin = nn.Linear(8, 5).to(device)
+    X = torch.randn(16, 8, generator=gen).to(device)
+    plain, scaled = KronTracker(lin), KronTracker(lin)
+    scaled.set_grad_scale(8.0)
+    scaled.enabled = False
+    with plain.track():
+        torch.autograd.grad(lin(X).pow(2).mean(), list(lin.parameters()))
+    plain.enabled = False
+    with scaled.track():
+        torch.autograd.grad(8.0 * lin(X).pow(2).mean(), list(lin.parameters()))
+    torch.testing.assert_close(scaled.factors[""]["G"], plain.factors[""]["G"], rtol=1e-5, atol=1e-8)
+    for bad in (0.0, -1.0, float("inf"), float("nan")):
+        with pytest.raises(ValueError, match="positive and finite"):
+            scaled.set_grad_scale(bad)
 
 
-def test_grad_scale_divides_out(device):
-    torch.manual_seed(4)
-    lin = nn.Linear(6, 3).to(device)
-    X, y = torch.randn(8, 6, device=device), torch.randn(8, 3, device=device)
-    t1, t2 = KronTracker(lin), KronTracker(lin)
-    t2.set_grad_scale(64.0)
-    with t1.track():
-        torch.autograd.grad(mse_half(lin(X), y), list(lin.parameters()))
-    t1.remove()
-    with t2.track():
-        torch.autograd.grad(64.0 * mse_half(lin(X), y), list(lin.parameters()))
-    assert torch.allclose(t1.factors[""]["G"], t2.factors[""]["G"], rtol=1e-5, atol=1e-7)
-    with pytest.raises(ValueError, match="positive and finite"):
-        t2.set_grad_scale(0.0)
+def test_capture_off_binds_nothing(device):
+    lin = nn.Linear(3, 3).to(device)
+    tr = KronTracker(lin)
+    tr.capture = False
+    with tr.track():
+        lin(torch.ones(2, 3, device=device)).sum().backward()
+    assert tr.factors == {} and tr.updates("") == 0
+    tr.remove()
+    tr.capture = True
+    with tr.track():  # hooks removed: still nothing
+        lin(torch.ones(2, 3, device=device)).sum().backward()
+    assert tr.factors == {}
 
 
 def test_bf16_activations_keep_fp32_factors(device):
-    torch.manual_seed(5)
-    lin = nn.Linear(16, 8).to(device)
-    X = torch.randn(32, 16, device=device)
+    """bf16 activations (an autocast region upstream) reach the hook as bf16
+    rows; the factor stays float32 and equals the Gram of those values."""
+    gen = torch.Generator().manual_seed(16)
+    lin = nn.Linear(32, 8).to(device)
+    Xb = torch.randn(64, 32, generator=gen).to(device).bfloat16()
     tr = KronTracker(lin)
     with tr.track():
         with torch.autocast(device_type=device.type, dtype=torch.bfloat16):
-            out = lin(X.bfloat16() if device.type == "cuda" else X)
-            loss = out.float().pow(2).mean()
+            loss = lin(Xb).float().square().mean()
         loss.backward()
     A = tr.factors[""]["A"]
     assert A.dtype == torch.float32
-    Xa = torch.cat([X, X.new_ones(32, 1)], 1)
-    Xa = Xa.bfloat16().float() if device.type == "cuda" else Xa
-    assert torch.allclose(A, Xa.T @ Xa / 32, atol=1e-5)
+    Xa = torch.cat([Xb.float(), torch.ones(64, 1, device=device)], 1)
+    torch.testing.assert_close(A, Xa.T @ Xa / 64, rtol=1e-5, atol=1e-5)

@@ -1,7 +1,15 @@
-"""SOAP: the reference's tests/test_soap.py identities (Adam when the factors
-stay diagonal, 1-D parameters are Adam, rotations change the path,
-convergence) on CPU and, on a GPU box, through the HIP kernels; plus
-teacher-forced steps against the numpy oracle across basis refreshes."""
+"""SOAP against closed forms, on CPU and, on a GPU box, through the HIP
+kernels (factor updates, eigenbasis rotations, second-moment transport):
+
+* gradients supported on one permutation pattern keep both factors
+  diagonal, their eigenbases are signed permutations, and elementwise Adam
+  commutes with those: SOAP is Adam;
+* with a single basis refresh (at step 0) SOAP is AdamW run on the rotated
+  gradients Q_Lᵀ·G·Q_R and rotated back;
+* vectors take the AdamW fallback (vs the numpy oracle);
+* teacher-forced steps against the numpy oracle across refreshes, and a
+  small regression that converges.
+"""
 
 import numpy as np
 import pytest
@@ -21,68 +29,108 @@ def _backend(device):
     ops.set_backend("auto")
 
 
-def test_equals_adam_when_factors_diagonal(device):
-    torch.manual_seed(0)
-    p_soap = nn.Parameter(torch.randn(5, 5, device=device))
-    p_adam = nn.Parameter(p_soap.detach().clone())
-    lr, betas, eps = 1e-2, (0.9, 0.999), 1e-8
-    soap = SOAP([p_soap], lr=lr, betas=betas, eps=eps, precondition_frequency=2)
-    adam = torch.optim.Adam([p_adam], lr=lr, betas=betas, eps=eps)
-    for t in range(7):
-        g = torch.diag(torch.randn(5, device=device))
-        p_soap.grad = g.clone()
-        p_adam.grad = g.clone()
+def _permutation_gradients(rows, cols, steps, seed, device):
+    """Gradients whose nonzeros sit on one fixed partial permutation: every
+    row and column has at most one entry, so G·Gᵀ and Gᵀ·G are diagonal."""
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(cols, generator=g)[:rows]
+    mask = torch.zeros(rows, cols)
+    mask[torch.arange(rows), perm] = 1.0
+    return [(mask * torch.randn(rows, cols, generator=g)).to(device) for _ in range(steps)]
+
+
+def test_permutation_supported_gradients_reduce_to_adam(device):
+    p0 = torch.randn(6, 9, generator=torch.Generator().manual_seed(1))
+    p_soap = nn.Parameter(p0.clone().to(device))
+    p_adam = nn.Parameter(p0.clone().to(device))
+    kw = dict(lr=2e-2, betas=(0.9, 0.99), eps=1e-8)
+    soap = SOAP([p_soap], precondition_frequency=3, **kw)
+    adam = torch.optim.Adam([p_adam], **kw)
+    for t, grad in enumerate(_permutation_gradients(6, 9, 8, 2, device)):
+        p_soap.grad, p_adam.grad = grad.clone(), grad.clone()
         soap.step()
         adam.step()
-        assert torch.allclose(p_soap.detach(), p_adam.detach(), atol=1e-6), t
+        torch.testing.assert_close(p_soap.detach(), p_adam.detach(), rtol=0, atol=2e-6, msg=f"step {t}")
 
 
-def test_1d_params_are_exactly_adam(device):
-    torch.manual_seed(1)
-    p_soap = nn.Parameter(torch.randn(9, device=device))
-    p_adam = nn.Parameter(p_soap.detach().clone())
-    soap = SOAP([p_soap], adamw_lr=3e-3, adamw_betas=(0.95, 0.95))
-    adam = torch.optim.Adam([p_adam], lr=3e-3, betas=(0.95, 0.95), eps=1e-8)
-    for _ in range(5):
-        g = torch.randn(9, device=device)
-        p_soap.grad = g.clone()
-        p_adam.grad = g.clone()
+def test_one_refresh_is_adamw_in_the_rotated_basis(device):
+    """precondition_frequency beyond the run: the basis from step 0 stays, so
+    from then on SOAP(p) = Q_L·AdamW(Q_Lᵀ·p·Q_R on rotated gradients)·Q_Rᵀ
+    (the decoupled decay is a scalar, rotation-invariant). AdamW starts from
+    SOAP's state after step 0 (rotated parameters and first moment, SOAP's
+    second moment, step 1): step 0 itself is not a fair comparison, since
+    its basis diagonalises g0, whose rotated off-diagonal entries are
+    rounding noise that m/(√v + ε) lifts to O(1)."""
+    gen = torch.Generator().manual_seed(3)
+    p0 = (0.1 * torch.randn(16, 24, generator=gen)).to(device)
+    grads = [torch.randn(16, 24, generator=gen).to(device) for _ in range(6)]
+    kw = dict(lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    p = nn.Parameter(p0.clone())
+    soap = SOAP([p], precondition_frequency=1000, **kw)
+    p.grad = grads[0]
+    soap.step()
+    st = soap.state[p]
+    QL, QR = st["Q_L"], st["Q_R"]
+    q = nn.Parameter(QL.T @ p.detach() @ QR)
+    adamw = torch.optim.AdamW([q], **kw)
+    adamw.state[q] = {"step": torch.tensor(1.0), "exp_avg": QL.T @ st["exp_avg"] @ QR,
+                      "exp_avg_sq": st["exp_avg_sq"].clone()}
+    for grad in grads[1:]:
+        p.grad = grad
         soap.step()
-        adam.step()
-    assert torch.allclose(p_soap.detach(), p_adam.detach(), atol=1e-6)
+        q.grad = QL.T @ grad @ QR
+        adamw.step()
+    torch.testing.assert_close(p.detach(), QL @ q.detach() @ QR.T, rtol=0, atol=2e-5)
+    assert st["step"] == 6
 
 
-def test_rotation_actually_used(device):
-    torch.manual_seed(2)
-    p_soap = nn.Parameter(torch.randn(4, 4, device=device))
-    p_adam = nn.Parameter(p_soap.detach().clone())
+def test_vectors_take_the_adamw_fallback(device):
+    gen = torch.Generator().manual_seed(4)
+    v0 = torch.randn(17, generator=gen)
+    v = nn.Parameter(v0.clone().to(device))
+    soap = SOAP([v], adamw_lr=3e-3, adamw_betas=(0.95, 0.95), adamw_wd=0.01)
+    want, m, s = v0.numpy(), np.zeros(17, np.float32), np.zeros(17, np.float32)
+    for t in range(1, 5):
+        grad = torch.randn(17, generator=gen)
+        v.grad = grad.to(device)
+        soap.step()
+        want, m, s = oopt.adamw_step(want, grad.numpy(), m, s, t, 3e-3, (0.95, 0.95), 1e-8, 0.01)
+    np.testing.assert_allclose(v.detach().cpu().numpy(), want, rtol=1e-6, atol=1e-7)
+    assert soap.diagnostics["n_adamw_params"] == 1
+
+
+def test_non_diagonal_gradients_move_away_from_adam(device):
+    gen = torch.Generator().manual_seed(5)
+    p0 = torch.randn(7, 7, generator=gen)
+    p_soap, p_adam = nn.Parameter(p0.clone().to(device)), nn.Parameter(p0.clone().to(device))
     soap = SOAP([p_soap], lr=1e-2, precondition_frequency=1)
     adam = torch.optim.Adam([p_adam], lr=1e-2, betas=(0.95, 0.95), eps=1e-8)
-    for _ in range(6):
-        g = torch.randn(4, 4, device=device)
-        p_soap.grad = g.clone()
-        p_adam.grad = g.clone()
+    for _ in range(5):
+        grad = torch.randn(7, 7, generator=gen).to(device)
+        p_soap.grad, p_adam.grad = grad.clone(), grad.clone()
         soap.step()
         adam.step()
-    assert not torch.allclose(p_soap.detach(), p_adam.detach(), atol=1e-4)
+    assert float((p_soap - p_adam).detach().norm()) > 1e-3
 
 
-def test_converges_small_regression(device):
-    torch.manual_seed(0)
-    X = torch.randn(256, 8, device=device)
-    W_true = torch.randn(8, 4, device=device)
-    y = torch.tanh(X @ W_true)
-    model = nn.Sequential(nn.Linear(8, 16), nn.Tanh(), nn.Linear(16, 4)).to(device)
-    opt = SOAP(model.parameters(), lr=1e-2, precondition_frequency=5)
-    losses = []
-    for _ in range(200):
+def test_trains_a_small_regression(device):
+    gen = torch.Generator().manual_seed(6)
+    X = torch.randn(320, 10, generator=gen).to(device)
+    Y = torch.tanh(0.5 * X @ torch.randn(10, 3, generator=gen).to(device))
+    torch.manual_seed(6)
+    model = nn.Sequential(nn.Linear(10, 24), nn.Tanh(), nn.Linear(24, 3)).to(device)
+    opt = SOAP(model.parameters(), lr=1e-2, precondition_frequency=4)
+    first = last = None
+    for _ in range(150):
         opt.zero_grad()
-        loss = 0.5 * (model(X) - y).pow(2).mean()
+        loss = (model(X) - Y).pow(2).mean()
         loss.backward()
         opt.step()
-        losses.append(float(loss.detach()))
-    assert losses[-1] < 0.15 * losses[0], (losses[0], losses[-1])
-    assert opt.diagnostics["n_adamw_params"] == 2 and opt.diagnostics["stale_steps"] <= 4
+        first = float(loss.detach()) if first is None else first
+        last = float(loss.detach())
+    assert last < 0.05 * first, (first, last)
+    diag = opt.diagnostics
+    assert diag["n_adamw_params"] == 2 and diag["stale_steps"] <= 3
 
 
 def test_teacher_forced_vs_oracle(device):
