@@ -10,7 +10,7 @@
 
 namespace pto {
 
-constexpr int kRedBlocks = 256;  // partial sums per matrix
+constexpr int kRedBlocks = 1024;  // partial sums per matrix
 
 // partial[b][blk] = sum of x^2 over rows blk, blk + kRedBlocks, ... of
 // matrix b (double accumulation, fixed order, so deterministic). Rows are
@@ -48,6 +48,22 @@ __global__ void __launch_bounds__(256) sumsq_partial_kernel(const T* __restrict_
     __syncthreads();
   }
   if (threadIdx.x == 0) partial[(int64_t)b * gridDim.x + blockIdx.x] = red[0];
+}
+
+// Sum of matrix b's kRedBlocks partials by the whole (256-thread) block in a
+// fixed order (each thread sums a strided quarter in index order, then a
+// tree), so the result is deterministic. Every thread gets the sum.
+__device__ __forceinline__ double block_sum_partials(const double* __restrict__ partial, int b) {
+  __shared__ double red[256];
+  double s = 0.0;
+  for (int i = threadIdx.x; i < kRedBlocks; i += 256) s += partial[(int64_t)b * kRedBlocks + i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  return red[0];
 }
 
 template <typename T>

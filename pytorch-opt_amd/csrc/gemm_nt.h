@@ -547,10 +547,11 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const int nrem = g.N - wc0;
   // direct runs: 8 lanes cover 64 consecutive columns of one row
   constexpr int RUNS = WTN / 8;  // 8-element runs per row
-  constexpr int LGD = RUNS < 8 ? RUNS : 8;
+  // lanes per output row: the largest divisor of RUNS that is at most 8
+  constexpr int LGD = RUNS % 8 == 0 ? 8 : RUNS % 6 == 0 ? 6 : RUNS % 4 == 0 ? 4 : RUNS % 2 == 0 ? 2 : 1;
   constexpr int RPB = 64 / LGD;
   constexpr int CBLK = RUNS / LGD;
-  static_assert(RUNS % LGD == 0, "wave tile width: at most 64 columns or a multiple of 64");
+  static_assert(RUNS % LGD == 0 && LGD * 8 <= 64, "wave tile width: whole 8-element runs");
   constexpr int ITEMS = ((RPP + RPB - 1) / RPB) * CBLK;  // direct runs per lane
   // when LGD does not divide 64 (wave tiles 48 wide) the last 64 % LGD lanes
   // would repeat the next block's first runs: they sit out

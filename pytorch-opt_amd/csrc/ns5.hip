@@ -68,17 +68,50 @@ int scratch_ptr(hipStream_t stream, void** ptr) {
   return 0;
 }
 
-// 1 / (sqrt(sum of partial squares) + eps), one thread per matrix.
+// 1 / (sqrt(sum of partial squares) + eps), one block per matrix.
 template <typename A>
-__global__ void ns_scale_kernel(const double* __restrict__ partial, int nblk, double eps, A* __restrict__ scale,
-                                int batch) {
-  int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= batch) return;
-  double s = 0.0;
-  for (int i = 0; i < nblk; ++i) s += partial[(int64_t)b * nblk + i];
-  A nrm = static_cast<A>(sqrt(s));
-  scale[b] = A(1) / (nrm + static_cast<A>(eps));
+__global__ void __launch_bounds__(256) ns_scale_kernel(const double* __restrict__ partial, double eps,
+                                                       A* __restrict__ scale) {
+  const double s = block_sum_partials(partial, blockIdx.x);
+  if (threadIdx.x == 0) scale[blockIdx.x] = A(1) / (static_cast<A>(sqrt(s)) + static_cast<A>(eps));
 }
+
+// A = s²·v: the first gram reads the input itself when no pack is needed,
+// so the 1/(‖G‖ + eps) scale lands here (scale == nullptr: A = v).
+template <typename T, typename A>
+struct EpiNsGram {
+  typedef A S;
+  T* dst;
+  int64_t ld, sd;
+  const A* scale;
+  bool vec;
+  typedef NoPre Pre;
+  typedef NoPre PreT;
+  static constexpr bool kVoIsV = true;
+  __device__ __forceinline__ bool has_t() const { return false; }
+  __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
+  __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
+  __device__ __forceinline__ void store(T* p, int b, const S* v, int kbeg, int n) const {
+    if (scale == nullptr) {
+      st8<T, S>(p, v, kbeg, n, vec);
+      return;
+    }
+    const S s2 = scale[b] * scale[b];
+    S w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = s2 * v[k];
+    st8<T, S>(p, w, kbeg, n, vec);
+  }
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre&, S* vo) const {
+    store(dst + (int64_t)b * sd + (int64_t)i * ld + j0, b, v, kbeg, n);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) vo[k] = v[k];
+  }
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT&) const {
+    store(dst + (int64_t)b * sd + (int64_t)j * ld + i0, b, v, 0, n);
+  }
+  __device__ __forceinline__ void finish(int) const {}
+};
 
 // B' = a·I + b·A + c·v  (symmetric, so the mirror takes the same value)
 template <typename T, typename A>
@@ -112,7 +145,9 @@ struct EpiNsSq {
   __device__ __forceinline__ void finish(int) const {}
 };
 
-// X' = v, stored to dst (row-major) and/or dstT (transposed copy).
+// X' = s·v (s per matrix, scale == nullptr: s = 1; the first update of an
+// unpacked input applies 1/(‖G‖ + eps) here), stored to dst (row-major)
+// and/or dstT (transposed copy).
 template <typename T, typename A>
 struct EpiNsUpdate {
   typedef A S;
@@ -121,19 +156,31 @@ struct EpiNsUpdate {
   T* dstT;
   int64_t ld_t, s_t;
   bool vec_d, vec_t;
+  const A* scale;
   typedef NoPre Pre;
   typedef NoPre PreT;
   static constexpr bool kVoIsV = true;
   __device__ __forceinline__ bool has_t() const { return dstT != nullptr; }
   __device__ __forceinline__ void load(int, int, int, int, int, Pre&) const {}
   __device__ __forceinline__ void load_t(int, int, int, int, PreT&) const {}
+  __device__ __forceinline__ void store(T* p, int b, const S* v, int kbeg, int n, bool vec) const {
+    if (scale == nullptr) {
+      st8<T, S>(p, v, kbeg, n, vec);
+      return;
+    }
+    const S s = scale[b];
+    S w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = s * v[k];
+    st8<T, S>(p, w, kbeg, n, vec);
+  }
   __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre&, S* vo) const {
 #pragma unroll
     for (int k = 0; k < 8; ++k) vo[k] = v[k];
-    if (dst) st8<T, S>(dst + (int64_t)b * s_d + (int64_t)i * ld_d + j0, v, kbeg, n, vec_d);
+    if (dst) store(dst + (int64_t)b * s_d + (int64_t)i * ld_d + j0, b, v, kbeg, n, vec_d);
   }
   __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT&) const {
-    st8<T, S>(dstT + (int64_t)b * s_t + (int64_t)j * ld_t + i0, v, 0, n, vec_t);
+    store(dstT + (int64_t)b * s_t + (int64_t)j * ld_t + i0, b, v, 0, n, vec_t);
   }
   __device__ __forceinline__ void finish(int) const {}
 };
@@ -211,7 +258,7 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
 
   // ‖X‖_F per matrix (deterministic two-stage sum), then 1/(‖X‖+eps).
   if (launch_sumsq<T>(G, rows, cols, cols, sG, nb, partial, stream)) return -1;
-  hipLaunchKernelGGL(ns_scale_kernel<A>, dim3((nb + 63) / 64), dim3(64), 0, stream, partial, kRedBlocks, eps, scale, nb);
+  hipLaunchKernelGGL(ns_scale_kernel<A>, dim3(nb), dim3(256), 0, stream, partial, eps, scale);
   PTO_LAUNCHED("ns_scale");
 
   if (steps == 0) {  // the normalised input, in the input's layout
@@ -219,8 +266,13 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
     return 0;
   }
 
-  // X0 = s·X (and, without the QN layout, X0ᵀ), pads zeroed.
-  if (QN) {
+  // X0 = s·X (and, without the QN layout, X0ᵀ), pads zeroed. bf16 inputs
+  // that need neither padding nor a transpose skip the copy: the first
+  // gram and update read G itself and apply s² and s in their epilogues.
+  const bool direct = QN && !transposed && m == ldm && n == ldn;
+  if (QN && direct) {
+    // no pads: X[1] is written in full by the first update
+  } else if (QN) {
     if (!transposed) {
       if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, X[0], ldn, sX, nullptr, 0, 0, false, nb, stream))
         return -1;
@@ -250,11 +302,14 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
   int cur = 0;  // X[cur] (QN) or XT[cur] holds the current iterate
   for (int64_t t = 0; t < steps; ++t) {
     const bool last = t == steps - 1;
-    T* Xc = X[cur];
+    // iteration 0 of an unpacked input reads G (stride sG == sX, no pads)
+    const bool from_g = direct && t == 0;
+    const T* Xc = from_g ? G : X[cur];
+    const A* s0 = from_g ? scale : nullptr;
     // 1. A = X·Xᵀ
     {
       GemmArgs g{Xc, ldn, sX, Xc, ldn, sX, (int)m, (int)m, (int)ldn, 0, 0, nullptr};
-      EpiStore<T, A> e{Ab, ldm, sAB, vec_ok<T>(Ab, ldm, sAB)};
+      EpiNsGram<T, A> e{Ab, ldm, sAB, s0, vec_ok<T>(Ab, ldm, sAB)};
       if (launch_gemm<T, true>(g, e, nb, stream, "ns5_gram")) return -1;
     }
     // 2. B' = a·I + b·A + c·A·A
@@ -275,6 +330,7 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
     //    transpose, X written in place since this product does not read it)
     {
       EpiNsUpdate<T, A> e{};
+      e.scale = s0;
       if (!last && QN) {
         e.dst = X[cur ^ 1]; e.ld_d = ldn; e.s_d = sX;
         e.dstT = nullptr;

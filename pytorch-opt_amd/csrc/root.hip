@@ -104,12 +104,11 @@ __global__ void __launch_bounds__(256) root_sym_kernel(const TI* __restrict__ A,
 
 // z = (1+p)/(2·max(‖M‖_F, tiny)), xs = z^(1/p), per matrix.
 template <typename R>
-__global__ void root_scale_kernel(const double* __restrict__ partial, int nblk, int p, R tiny, R* __restrict__ z,
-                                  R* __restrict__ xs, int batch) {
-  int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= batch) return;
-  double s = 0.0;
-  for (int i = 0; i < nblk; ++i) s += partial[(int64_t)b * nblk + i];
+__global__ void __launch_bounds__(256) root_scale_kernel(const double* __restrict__ partial, int p, R tiny,
+                                                         R* __restrict__ z, R* __restrict__ xs) {
+  const int b = blockIdx.x;
+  const double s = block_sum_partials(partial, b);
+  if (threadIdx.x != 0) return;
   R fro = static_cast<R>(sqrt(s));
   if (fro < tiny) fro = tiny;  // clamp_min; NaN compares false and passes through
   R zz = static_cast<R>(1.0 + p) / (R(2) * fro);
@@ -320,8 +319,8 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     PTO_LAUNCHED("root_sym");
   }
   if (launch_sumsq<R>(M, n, n, ld, sb, nb, partial, stream)) return -1;
-  hipLaunchKernelGGL(root_scale_kernel<R>, dim3((nb + 63) / 64), dim3(64), 0, stream, partial, kRedBlocks, (int)p,
-                     std::numeric_limits<R>::min(), z, xs, nb);
+  hipLaunchKernelGGL(root_scale_kernel<R>, dim3(nb), dim3(256), 0, stream, partial, (int)p,
+                     std::numeric_limits<R>::min(), z, xs);
   PTO_LAUNCHED("root_scale");
   {
     unsigned blocks = (unsigned)std::min<int64_t>((sb + 255) / 256, 2048);
