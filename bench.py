@@ -435,6 +435,46 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "ns5_bf16_traffic.json")
 COPY_BYTES = 1 << 30  # calibration copy: 1 GiB read + 1 GiB written
 
 
+def kernel_probe(torch, ops, hip, dev, which):
+    """A bounded run of one kernel family, for rocprofv3 (no timing output):
+    factors  fp32 Kronecker update of G 4096² (beta 0.95) x10 and the K-FAC
+             Gram of bf16 A 16384x4096 into fp32 x10;
+    roots    the config-4 fp32 coupled-Newton roots at n = 1024, 2048, 4096
+             (100 iterations each), twice;
+    ns5      the headline step (32 x 4096² + 32 x 4096x11008 bf16) x3 and one
+             4096² matrix x10."""
+    if which == "factors":
+        g = torch.Generator(device=dev).manual_seed(2)
+        G = 1e-2 * torch.randn(4096, 4096, generator=g, device=dev)
+        L, R = G @ G.T, G.T @ G
+        A = torch.randn(16384, 4096, generator=torch.Generator(device=dev).manual_seed(3), device=dev).bfloat16()
+        F = torch.zeros(4096, 4096, device=dev)
+        for _ in range(10):
+            ops.kron_factor_update_(L, R, G, beta2=0.95)
+        for _ in range(10):
+            ops.gram_update_(F, A, beta=0.95, alpha=0.05 / 16384)
+    elif which == "roots":
+        for n in (1024, 2048, 4096):
+            g = torch.Generator().manual_seed(4)
+            Q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+            lam = 10 ** (-6 * torch.rand(n, generator=torch.Generator().manual_seed(5), dtype=torch.float64))
+            A = ((Q * lam) @ Q.T).float().to(dev)
+            for _ in range(2):
+                hip.inverse_matrix_root_iters(A, 4, 1e-6, "newton", False, 100, 1e-10)
+    elif which == "ns5":
+        inputs = [make_ns5_inputs(torch, b, r, c, s, dev) for b, r, c, s in SHAPES]
+        for _ in range(3):
+            for G in inputs:
+                ops.newton_schulz_orthogonalize(G)
+        single = inputs[0][:1].contiguous()
+        for _ in range(10):
+            ops.newton_schulz_orthogonalize(single)
+    else:
+        raise SystemExit(f"unknown probe {which!r}")
+    torch.cuda.synchronize()
+    print(f"probe {which} done", flush=True)
+
+
 def traffic_probe(torch, ops, dev):
     """One NS5 step of the headline workload and a 1 GiB device copy, for
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
@@ -495,6 +535,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="headline only (no factors/roots/optimizer)")
     ap.add_argument("--opt-steps", type=int, default=40)
     ap.add_argument("--traffic-probe", action="store_true", help="one NS5 step + 1 GiB copy, for PMC runs")
+    ap.add_argument("--probe", choices=("factors", "roots", "ns5"), help="a bounded run of one kernel family "
+                    "for rocprofv3, no timing")
     ap.add_argument("--digest-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the ns5_update HBM traffic summary from two PMC runs")
     args = ap.parse_args()
@@ -516,9 +558,12 @@ def main():
     hip = ops._NATIVE
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    cpu = None if args.no_cpu_baseline else cpu_setup(torch)
+    cpu = None if (args.no_cpu_baseline or args.probe or args.traffic_probe) else cpu_setup(torch)
     if args.traffic_probe:
         traffic_probe(torch, ops, dev)
+        return
+    if args.probe:
+        kernel_probe(torch, ops, hip, dev, args.probe)
         return
     inputs = [make_ns5_inputs(torch, b, r, c, s, dev) for b, r, c, s in SHAPES]
     torch.cuda.synchronize()
