@@ -6,8 +6,9 @@
 // fragment a contiguous 16-byte run in LDS for all three element types.
 //
 // Operand contract (checked by the host launchers):
-//   * K is a multiple of four K tiles (kStages * BK) and the pad columns of
-//     both operands are zero (workspace buffers are padded to kPadK);
+//   * K is a multiple of one ring of K tiles (Tile::NS * BK) and the pad
+//     columns of both operands are zero (workspace buffers are padded to
+//     kPadK);
 //   * rows beyond M (P) or N (Q) are never read (masked to zero);
 //   * operand base pointers and leading dimensions are 16-byte aligned.
 //
@@ -16,8 +17,9 @@
 // for (i, j), i <= j, is stored at (i, j) and at (j, i), so the result is an
 // exactly symmetric matrix at half the MFMA work.
 //
-// Pipeline: a ring of four LDS stages filled by direct global-to-LDS loads,
-// three K tiles ahead of the MFMAs; one barrier per K tile (details below).
+// Pipeline: a ring of LDS stages (four, or eight for the small fp32/fp64
+// tiles) filled by direct global-to-LDS loads, NS - 1 K tiles ahead of the
+// MFMAs; one barrier per K tile (details below).
 #pragma once
 
 #include <atomic>
@@ -92,11 +94,13 @@ struct Mfma<double> {  // v_mfma_f64_16x16x4_f64
   __device__ static __forceinline__ int col(int lane, int) { return lane & 15; }
 };
 
-// Tile configuration: BM x BN output tile, BK deep (64 bytes), WM x WN waves.
-template <int BM_, int BN_, int BK_, int WM_, int WN_>
+// Tile configuration: BM x BN output tile, BK deep (64 bytes), WM x WN
+// waves, NS LDS stages (4 or 8).
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_ = 4>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
   static constexpr int NT = 64 * WM * WN;
+  static_assert(NS == 4 || NS == 8, "ring of 4 or 8 stages");
 };
 
 struct GemmArgs {
@@ -148,20 +152,25 @@ __device__ __forceinline__ void decode_tile(int t, int tiles_m, int tiles_n, int
 // ------------------------------------------------------------- main loop
 // K tiles are 64 bytes deep (bf16 BK=32, fp32 16, fp64 8). Operand tiles
 // go from global memory straight into LDS (global_load_lds_dwordx4: each
-// wave instruction fills 1 KiB = 16 rows of 64 bytes) through a ring of
-// four stages, so three tiles are in flight while one is consumed, with no
+// wave instruction fills 1 KiB = 16 rows of 64 bytes) through a ring of NS
+// stages, so NS - 1 tiles are in flight while one is consumed, with no
 // staging registers and no ds_write instructions. The stages are separate
-// __shared__ arrays and the loop is unrolled by four, so every LDS access
+// __shared__ arrays and the loop is unrolled by NS, so every LDS access
 // names its stage statically and the compiler's wait insertion can tell the
 // in-flight stages apart; prefetches are unconditional (past the end they
 // re-read the last tile into a stage that is never consumed) so the
 // outstanding-load count is the same on every path.
 //
+// A tile's load is issued NS - 2 steps before its LDS reads, so a step
+// cannot be shorter than the load latency / (NS - 2). The big tiles' steps
+// (512+ MFMA cycles per wave) cover it with four stages; the small fp32 and
+// fp64 tiles (128-512 cycles per step) use eight.
+//
 // LDS rows are unpadded; 16-byte chunk c of row r lives at physical chunk
 // c ^ f(r), f(r) = ((r >> 2) & 3) ^ (r & 2), which makes the fragment
 // reads (16 consecutive rows, one chunk) conflict-free in both 8- and
 // 16-lane windows. The DMA side needs no care: it writes 1 KiB runs.
-constexpr int kStages = 4;
+constexpr int kStages = 4;  // the default ring
 constexpr int kRowBytes = 64;
 
 __device__ __forceinline__ int swz(int r) { return ((r >> 2) & 3) ^ (r & 2); }
@@ -216,15 +225,15 @@ __device__ __forceinline__ void stage_barrier() {
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) const void gbl_void_t;
 
-// LDS plan: four stages of (BM + BN) rows x 64 bytes; after the loop each
+// LDS plan: NS stages of (BM + BN) rows x 64 bytes; after the loop each
 // stage array also hosts the epilogue staging of WPA waves (RPP rows x
 // (WTN + 1) accumulator-type values per wave, odd pitch).
 template <typename T, class Cfg, typename S>
 struct LdsPlan {
-  static constexpr int NW = Cfg::WM * Cfg::WN;
+  static constexpr int NW = Cfg::WM * Cfg::WN, NS = Cfg::NS;
   static constexpr int WTM = Cfg::BM / Cfg::WM, WTN = Cfg::BN / Cfg::WN;
   static constexpr int STAGE = (Cfg::BM + Cfg::BN) * kRowBytes;
-  static constexpr int WPA = (NW + kStages - 1) / kStages;  // waves per array in the epilogue
+  static constexpr int WPA = (NW + NS - 1) / NS;  // waves per array in the epilogue
   static constexpr int SP = WTN + 1;
   static constexpr int kLdsMax = 160 * 1024;
   // rows per epilogue pass: the largest multiple of 16, at most 64, that
@@ -232,7 +241,7 @@ struct LdsPlan {
   static constexpr int pick_rpp() {
     for (int r = (WTM < 64 ? WTM : 64) / 16 * 16; r > 16; r -= 16) {
       const int epi = WPA * r * SP * (int)sizeof(S);
-      if (WTM % r == 0 && kStages * (STAGE > epi ? STAGE : epi) <= kLdsMax) return r;
+      if (WTM % r == 0 && NS * (STAGE > epi ? STAGE : epi) <= kLdsMax) return r;
     }
     return 16;
   }
@@ -269,17 +278,24 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
                 "PT layout: with QN, P rows of 256·k or 256·k + 128 bytes");
   static_assert(WTM % MF::MN == 0 && WTN % MF::MN == 0 && WTM % 16 == 0, "wave tile");
   static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
-  static_assert(3 * IPW <= 63, "vmcnt range");
+  constexpr int NS = Cfg::NS;
+  static_assert((NS - 2) * IPW <= 63, "vmcnt range");
   static_assert(Plan::RPP % MF::MN == 0 && WTM % Plan::RPP == 0, "epilogue passes");
-  static_assert(kStages * Plan::ARR <= Plan::kLdsMax, "LDS budget");
+  static_assert(Cfg::NS * Plan::ARR <= Plan::kLdsMax, "LDS budget");
   static_assert(!QN || (sizeof(T) == 2 && (!UPPER || PT) && CPR >= 16 && (QRB % 256 == 0 || QRB % 256 == 128) &&
                         (BM * kRowBytes) % 1024 == 0 && NRG == 1),
                 "QN layout: bf16, Q rows of 256·k or 256·k + 128 bytes; symmetric products only with PT");
 
+  // stages 4..7 exist (at full size) only in eight-stage rings
+  constexpr int ARR_HI = NS > 4 ? Plan::ARR : 16;
   __shared__ __attribute__((aligned(16))) char st0[Plan::ARR];
   __shared__ __attribute__((aligned(16))) char st1[Plan::ARR];
   __shared__ __attribute__((aligned(16))) char st2[Plan::ARR];
   __shared__ __attribute__((aligned(16))) char st3[Plan::ARR];
+  __shared__ __attribute__((aligned(16))) char st4[ARR_HI];
+  __shared__ __attribute__((aligned(16))) char st5[ARR_HI];
+  __shared__ __attribute__((aligned(16))) char st6[ARR_HI];
+  __shared__ __attribute__((aligned(16))) char st7[ARR_HI];
 
   const int tid = threadIdx.x;
   // wave index in a scalar register: DMA destinations and per-wave offsets
@@ -471,31 +487,38 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
 
   // Skewed pipeline: during step s the wave issues the LDS reads of tile
   // s+1 into one register set, then the MFMAs of tile s from the other set
-  // (read during step s-1), with the DMA of tile s+3 spread between them;
-  // LDS latency hides behind a whole tile of MFMAs and the memory unit's
-  // queue never holds up MFMA issue. One barrier per step covers both
-  // hazards: every wave has waited for its reads (lgkmcnt(0)) before
+  // (read during step s-1), with the DMA of tile s+NS-1 spread between
+  // them; LDS latency hides behind a whole tile of MFMAs and the memory
+  // unit's queue never holds up MFMA issue. One barrier per step covers
+  // both hazards: every wave has waited for its reads (lgkmcnt(0)) before
   // arriving, so the stage of tile s-1 may be refilled, and every wave's
-  // part of tile s+1 has landed (vmcnt: only tile s+2 may be outstanding).
-  // The launchers require K to be a multiple of four tiles, so every step
-  // of the unrolled group is a real one and the MFMAs need no branch.
+  // part of tile s+1 has landed (vmcnt: only tiles s+2 .. s+NS-2 may be
+  // outstanding). The launchers require K to be a multiple of NS tiles, so
+  // every step of the unrolled group is a real one and the MFMAs need no
+  // branch.
   const int KT = g.K / BK;
   if (KT > 0) {
     Frag f0, f1;
     issue(0, st0);
     issue(min(1, KT - 1), st1);
     issue(min(2, KT - 1), st2);
-    __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));
+    if constexpr (NS == 8) {
+      issue(min(3, KT - 1), st3);
+      issue(min(4, KT - 1), st4);
+      issue(min(5, KT - 1), st5);
+      issue(min(6, KT - 1), st6);
+    }
+    __builtin_amdgcn_s_waitcnt(PTO_VMCNT((NS - 2) * IPW));
     stage_barrier();
     load_frags(st0, f0);
-    for (int kt = 0; kt < KT; kt += kStages) {
+    for (int kt = 0; kt < KT; kt += NS) {
       // J: step in the unrolled group; RD: stage of tile kt+J+1; DMA:
-      // stage of tile kt+J+3
+      // stage of tile kt+J+NS-1
 #define PTO_STEP(J, CUR, NXT, RD, DMA)                                \
-  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(IPW));                         \
+  __builtin_amdgcn_s_waitcnt(PTO_VMCNT((NS - 3) * IPW));              \
   stage_barrier();                                                    \
   load_frags(RD, NXT);                                                \
-  issue(min(kt + (J) + 3, KT - 1), DMA);                              \
+  issue(min(kt + (J) + NS - 1, KT - 1), DMA);                         \
   mma(CUR);                                                           \
   if constexpr (!kSpreadReads)                                        \
     __builtin_amdgcn_sched_group_barrier(0x100, kFragReads, 0);       \
@@ -505,10 +528,21 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                \
     __builtin_amdgcn_sched_group_barrier(0x008, kTileMfma / IPW, 0);  \
   }
-      PTO_STEP(0, f0, f1, st1, st3)
-      PTO_STEP(1, f1, f0, st2, st0)
-      PTO_STEP(2, f0, f1, st3, st1)
-      PTO_STEP(3, f1, f0, st0, st2)
+      if constexpr (NS == 4) {
+        PTO_STEP(0, f0, f1, st1, st3)
+        PTO_STEP(1, f1, f0, st2, st0)
+        PTO_STEP(2, f0, f1, st3, st1)
+        PTO_STEP(3, f1, f0, st0, st2)
+      } else {
+        PTO_STEP(0, f0, f1, st1, st7)
+        PTO_STEP(1, f1, f0, st2, st0)
+        PTO_STEP(2, f0, f1, st3, st1)
+        PTO_STEP(3, f1, f0, st4, st2)
+        PTO_STEP(4, f0, f1, st5, st3)
+        PTO_STEP(5, f1, f0, st6, st4)
+        PTO_STEP(6, f0, f1, st7, st5)
+        PTO_STEP(7, f1, f0, st0, st6)
+      }
 #undef PTO_STEP
     }
     __builtin_amdgcn_s_waitcnt(PTO_VMCNT(0));  // stray prefetches land before reuse
@@ -539,7 +573,8 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // on diagonal tiles positions below the diagonal are skipped by the
   // direct pass, so the stored matrix is exactly symmetric.
   constexpr int RPP = Plan::RPP, SP = Plan::SP;
-  char* arr = (wave / Plan::WPA) == 0 ? st0 : (wave / Plan::WPA) == 1 ? st1 : (wave / Plan::WPA) == 2 ? st2 : st3;
+  const int wa = wave / Plan::WPA;  // < NS
+  char* arr = wa == 0 ? st0 : wa == 1 ? st1 : wa == 2 ? st2 : wa == 3 ? st3 : wa == 4 ? st4 : wa == 5 ? st5 : wa == 6 ? st6 : st7;
   S* stg = reinterpret_cast<S*>(arr) + (wave % Plan::WPA) * RPP * SP;
   const bool diag = UPPER && ti == tj;
   const bool need_t = UPPER || epi.has_t();
@@ -659,20 +694,27 @@ struct TileSet<bf16> {
   typedef Tile<256, 256, 32, 2, 4> sym_big;
   typedef Tile<128, 128, 32, 2, 2> sym_small;
   typedef Tile<192, 192, 32, 2, 4> sym_mid;
-  static constexpr bool kHasMid = true;
+  typedef sym_small sym_tiny;  // unused
+  static constexpr bool kHasMid = true, kHasTiny = false;
   static constexpr double kBigRate = 1.5;
   static constexpr double kMidRate = 1.35;
+  static constexpr double kTinyRate = 0.0;
 };
+// fp32 symmetric products also have a 32 x 32 "tiny" tile (4 waves of
+// 16 x 16): an n = 1024 product is 136 upper tiles of 64² (120 of 256 CUs
+// idle) but 528 of 32², about two co-resident workgroups per CU.
 template <>
 struct TileSet<float> {
   typedef Tile<128, 128, 16, 2, 2> big;
-  typedef Tile<64, 64, 16, 2, 2> small;
+  typedef Tile<64, 64, 16, 2, 2, 8> small;
   typedef big sym_big;
   typedef small sym_small;
   typedef Tile<192, 192, 16, 2, 4> sym_mid;
-  static constexpr bool kHasMid = true;
+  typedef Tile<32, 32, 16, 2, 2, 8> sym_tiny;
+  static constexpr bool kHasMid = true, kHasTiny = true;
   static constexpr double kBigRate = 1.22;
   static constexpr double kMidRate = 1.3;
+  static constexpr double kTinyRate = 0.85;
 };
 template <>
 struct TileSet<double> {
@@ -680,11 +722,28 @@ struct TileSet<double> {
   typedef Tile<32, 32, 8, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
-  typedef big sym_mid;  // unused
-  static constexpr bool kHasMid = false;
+  typedef big sym_mid;    // unused
+  typedef small sym_tiny;  // unused
+  static constexpr bool kHasMid = false, kHasTiny = false;
   static constexpr double kBigRate = 1.25;
   static constexpr double kMidRate = 0.0;
+  static constexpr double kTinyRate = 0.0;
 };
+
+// K granularity of a type's products: every tile's ring of K tiles (at
+// most kPadK elements, the pitch every operand buffer is padded to).
+template <typename T>
+constexpr int ring_k() {
+  typedef TileSet<T> S;
+  int r = 0;
+  for (int v : {S::big::NS * S::big::BK, S::small::NS * S::small::BK, S::sym_big::NS * S::sym_big::BK,
+                S::sym_small::NS * S::sym_small::BK, S::sym_mid::NS * S::sym_mid::BK,
+                S::sym_tiny::NS * S::sym_tiny::BK})
+    r = v > r ? v : r;
+  return r;
+}
+static_assert(kPadK % ring_k<bf16>() == 0 && kPadK % ring_k<float>() == 0 && kPadK % ring_k<double>() == 0,
+              "padded K covers every ring");
 
 // Compute units of the current device (256 on a full MI355X), cached per
 // device ordinal.
@@ -751,7 +810,14 @@ int pick_tile(int64_t M, int64_t N, int64_t batch) {
     best = big;
     pick = 1;
   }
-  if (UPPER && TileSet<T>::kHasMid && load(Mid::BM, Mid::BN, TileSet<T>::kMidRate) < best) pick = 2;
+  if (UPPER && TileSet<T>::kHasMid && load(Mid::BM, Mid::BN, TileSet<T>::kMidRate) < best) {
+    best = load(Mid::BM, Mid::BN, TileSet<T>::kMidRate);
+    pick = 2;
+  }
+  if (UPPER && TileSet<T>::kHasTiny) {
+    typedef typename TileSet<T>::sym_tiny Tiny;
+    if (load(Tiny::BM, Tiny::BN, TileSet<T>::kTinyRate) < best) pick = 3;
+  }
   return pick;
 }
 
@@ -764,7 +830,7 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
   static_assert(!UPPER || (Big::BM == Big::BN && Small::BM == Small::BN), "symmetric products need square tiles");
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
   PTO_REQUIRE(!UPPER || g.M == g.N, std::string(name) + ": symmetric product needs M == N");
-  PTO_REQUIRE(g.K % (kStages * Small::BK) == 0 && g.K % (kStages * Big::BK) == 0, std::string(name) + ": K not padded");
+  PTO_REQUIRE(g.K % ring_k<T>() == 0, std::string(name) + ": K not padded");
   PTO_REQUIRE(g.ldp % (16 / sizeof(T)) == 0 && g.ldq % (16 / sizeof(T)) == 0 &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 &&
                   (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
@@ -774,6 +840,11 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
     typedef typename TileSet<T>::sym_mid Mid;
     static_assert(Mid::BM == Mid::BN && Mid::BK == Big::BK, "mid tile: square, same K tile");
     if (pick == 2) return launch_gemm_cfg<T, Mid, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
+  }
+  if constexpr (UPPER && TileSet<T>::kHasTiny) {
+    typedef typename TileSet<T>::sym_tiny Tiny;
+    static_assert(Tiny::BM == Tiny::BN && Tiny::BK == Big::BK, "tiny tile: square, same K tile");
+    if (pick == 3) return launch_gemm_cfg<T, Tiny, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
   }
   if (pick == 1) return launch_gemm_cfg<T, Big, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
   return launch_gemm_cfg<T, Small, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
@@ -793,7 +864,7 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
   typedef typename PickTiles<bf16, UPPER>::Small Small;
   PTO_REQUIRE(g.M >= 0 && g.N >= 0 && g.K >= 0, std::string(name) + ": negative extent");
   PTO_REQUIRE(!UPPER || g.M == g.N, std::string(name) + ": symmetric product needs M == N");
-  PTO_REQUIRE(g.K % (kStages * Big::BK) == 0 && g.K % (kStages * Small::BK) == 0, std::string(name) + ": K not padded");
+  PTO_REQUIRE(g.K % ring_k<bf16>() == 0, std::string(name) + ": K not padded");
   PTO_REQUIRE(g.ldq < (int64_t(1) << 26) && g.ldp < (int64_t(1) << 26),
               std::string(name) + ": row pitch too large");  // 64-byte K steps in 32 bits
   PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 && (!PT || (g.ldp >= g.M && g.ldp >= 8)) &&

@@ -347,20 +347,39 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     return launch_gemm<R, false, EpiStore<R, R>, true>(g, e, nb, stream, name);
   };
 
+  // One matrix, p >= 2: X·Mi and the first power product Mi·Mi share their
+  // Q operand (Mi), so they run as one launch of two "matrices" whose P and
+  // output strides are the buffers' distances (twice the workgroups for a
+  // one-matrix launch that would leave CUs idle; each product's arithmetic
+  // is unchanged).
+  const bool pair = nb == 1 && p >= 2;
+  auto product_pair = [&](const R* P0, R* d0, const R* P1, R* d1, const R* Q, const char* name) -> int {
+    GemmArgs g{P0, ld, (int64_t)(P1 - P0), Q, ld, 0, (int)n, (int)n, (int)ld, 0, 0, guard, 0};
+    const int64_t sd = (int64_t)(d1 - d0);
+    EpiStore<R, R> e{d0, ld, sd, vec_ok<R>(d0, ld, sd)};
+    return launch_gemm<R, true, EpiStore<R, R>, true>(g, e, 2, stream, name);
+  };
+
   auto iteration = [&](int it) -> int {
     const int cur = it & 1, nxt = cur ^ 1;
-    // X_{it+1} = X_it · Mi (symmetric: both are polynomials in M)
-    if (product(X[cur], Mi[cur], X[nxt], true, "root_xmi")) return -1;
+    // X_{it+1} = X_it · Mi (symmetric: both are polynomials in M); with
+    // `pair`, tmp[0] = Mi·Mi in the same launch
+    if (pair) {
+      if (product_pair(X[cur], X[nxt], Mi[cur], tmp[0], Mi[cur], "root_xmi_pow")) return -1;
+    } else if (product(X[cur], Mi[cur], X[nxt], true, "root_xmi")) {
+      return -1;
+    }
     // S = Mi^p (torch.linalg.matrix_power order: direct for p <= 3, else
-    // binary powering from the least significant bit)
+    // binary powering from the least significant bit; its first product is
+    // always Mi·Mi, into tmp[0])
     const R* S = nullptr;
     if (p == 1) {
       S = Mi[cur];
     } else if (p == 2) {
-      if (product(Mi[cur], Mi[cur], tmp[0], true, "root_pow")) return -1;
+      if (!pair && product(Mi[cur], Mi[cur], tmp[0], true, "root_pow")) return -1;
       S = tmp[0];
     } else if (p == 3) {
-      if (product(Mi[cur], Mi[cur], tmp[0], true, "root_pow")) return -1;
+      if (!pair && product(Mi[cur], Mi[cur], tmp[0], true, "root_pow")) return -1;
       if (product(tmp[0], Mi[cur], tmp[1], true, "root_pow")) return -1;
       S = tmp[1];
     } else {
@@ -379,7 +398,11 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
           zp = Mi[cur];
         } else {
           R* d = free_tmp();
-          if (product(zp, zp, d, true, "root_pow")) return -1;
+          if (pair && zp == Mi[cur]) {
+            PTO_REQUIRE(d == tmp[0], "inverse_matrix_root: power buffers");  // Mi·Mi is there already
+          } else if (product(zp, zp, d, true, "root_pow")) {
+            return -1;
+          }
           zp = d;
         }
         if (bit) {
