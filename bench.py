@@ -147,7 +147,7 @@ def bench_factors(torch, ops, hip, dev, cpu):
         ("kron_update_fp32_4096", lambda: ops.kron_factor_update_(L, R, G, beta2=0.95), 2 * 4096 * 4097 * 4096,
          "fp32", ("kron_left", "kron_right")),
         ("kfac_gram_bf16_16384x4096", lambda: ops.gram_update_(F, A, beta=0.95, alpha=0.05 / 16384),
-         4096 * 4097 * 16384, "bf16", ("gram_update",))]:
+         4096 * 4097 * 16384, "bf16", ("gram_update", "gram_update_direct"))]:
         fn()
         torch.cuda.synchronize()
         hip.prof_reset()

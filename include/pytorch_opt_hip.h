@@ -91,6 +91,9 @@ int pto_kron_factor_update(void* L, void* R, const void* G, int dtype, int64_t m
  * EMA / running-mean step :95-103 (beta == 0 overwrites F).
  * X [rows, d] of x_dtype, F [d(+1), d(+1)] of f_dtype.
  * Supported (x, F) pairs: (bf16, f32), (f32, f32), (f64, f64).
+ * The workspace size is 0 when X is read in place (bf16, rows % 128 == 0,
+ * d % 8 == 0, no ones column, and the tile the library picks for d allows
+ * it); X must then be 16-byte aligned, and workspace may be NULL.
  */
 size_t pto_gram_workspace_bytes(int x_dtype, int64_t rows, int64_t d, int append_ones);
 int pto_gram_update(void* F, int f_dtype, const void* X, int x_dtype, int64_t rows, int64_t d, int append_ones,

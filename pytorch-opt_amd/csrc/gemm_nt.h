@@ -857,8 +857,10 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
 // ldp >= M, K rows, the rows past the true K zero) — for a symmetric P
 // that is P itself. UPPER (with PT): a symmetric product on upper tiles,
 // mirrored, as in launch_gemm.
+// pick: the tile (pick_tile's codes), or -1 to let pick_tile choose.
 template <class Epi, bool PT = false, bool UPPER = false>
-int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
+int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream, const char* name,
+                   int pick = -1) {
   static_assert(PT || !UPPER, "symmetric QN products need PT");
   typedef typename PickTiles<bf16, UPPER>::Big Big;
   typedef typename PickTiles<bf16, UPPER>::Small Small;
@@ -870,7 +872,8 @@ int launch_gemm_qn(const GemmArgs& g, const Epi& epi, int batch, hipStream_t str
   PTO_REQUIRE(g.ldp % 8 == 0 && g.ldq % 8 == 0 && g.ldq >= g.N && g.ldq >= 8 && (!PT || (g.ldp >= g.M && g.ldp >= 8)) &&
                   (reinterpret_cast<uintptr_t>(g.P) & 15) == 0 && (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
-  const int pick = pick_tile<bf16, UPPER>(g.M, g.N, batch);
+  PTO_REQUIRE(pick >= -1 && pick <= 2 && (UPPER || pick != 2), std::string(name) + ": tile choice");
+  if (pick < 0) pick = pick_tile<bf16, UPPER>(g.M, g.N, batch);
   if constexpr (UPPER) {
     // the 192² tile: 384-byte transposing rows (swzq's second form)
     typedef typename TileSet<bf16>::sym_mid Mid;

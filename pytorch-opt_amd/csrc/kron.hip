@@ -67,8 +67,24 @@ int kron_t(T* L, T* R, const T* G, int64_t m, int64_t n, double beta2, void* ws,
   return 0;
 }
 
+// bf16 X without the ones column is already the [K][M] operand of the
+// transposing-read layout (K = tokens, M = features), for both sides of
+// X̃ᵀX̃: it is read in place, with no Xᵀ pass and no workspace, when the
+// token count needs no pad rows, the rows are whole 16-byte chunks and the
+// tile model picks the 192² or 128² tile (the 256² tile spills with the
+// fp32 blend epilogue on this layout). Returns that tile (pick_tile's code)
+// or -1 for the packed path. X's 16-byte alignment is the caller's part of
+// the contract (checked at launch).
+template <typename TX>
+int gram_direct_tile(int64_t rows, int64_t d, int append_ones) {
+  if (sizeof(TX) != 2 || append_ones || rows % kPadK != 0 || d % 8 != 0 || d == 0) return -1;
+  const int pick = pick_tile<TX, true>(d, d, 1);
+  return pick == 0 || pick == 2 ? pick : -1;
+}
+
 template <typename TX>
 size_t gram_ws_bytes_t(int64_t rows, int64_t d, int append_ones) {
+  if (gram_direct_tile<TX>(rows, d, append_ones) >= 0) return 0;
   int64_t dd = d + (append_ones ? 1 : 0);
   return sizeof(TX) * dd * round_up(rows, kPadK) + 512;
 }
@@ -82,23 +98,19 @@ int gram_t(TF* F, const TX* X, int64_t rows, int64_t d, int append_ones, double 
   PTO_REQUIRE(dd <= INT32_MAX && rows <= INT32_MAX, "gram_update_: shape too large");
   if (dd == 0) return 0;
   const int64_t ldr = round_up(rows, kPadK);
+  if constexpr (sizeof(TX) == 2) {
+    const int tile = gram_direct_tile<TX>(rows, d, append_ones);
+    if (tile >= 0) {
+      PTO_REQUIRE((reinterpret_cast<uintptr_t>(X) & 15) == 0,
+                  "gram_update_: X must be 16-byte aligned (it is read in place)");
+      GemmArgs g{X, d, 0, X, d, 0, (int)dd, (int)dd, (int)rows, 0, 0, nullptr};
+      EpiBlend<TF, A> e{F, dd, 0, static_cast<A>(beta), static_cast<A>(alpha), vec_ok<TF>(F, dd, 0)};
+      return launch_gemm_qn<EpiBlend<TF, A>, true, true>(g, e, 1, stream, "gram_update_direct", tile);
+    }
+  }
   Carver cv(ws, ws_bytes);
   TX* XT = cv.take<TX>(dd * ldr);
   PTO_REQUIRE(!cv.overflow, "gram_update_: workspace too small");
-  // bf16 X without the ones column is already the [K][M] operand of the
-  // transposing-read layout (K = tokens, M = features), for both sides of
-  // X̃ᵀX̃: read it in place, no Xᵀ pass, when the token count needs no pad
-  // rows and the rows are whole 16-byte chunks. The 256² tile would spill
-  // with the fp32 blend epilogue on this layout, so only the 192² and 128²
-  // tiles take it.
-  if constexpr (sizeof(TX) == 2) {
-    if (!append_ones && rows % kPadK == 0 && d % 8 == 0 && (reinterpret_cast<uintptr_t>(X) & 15) == 0 &&
-        pick_tile<TX, true>(dd, dd, 1) != 1) {
-      GemmArgs g{X, d, 0, X, d, 0, (int)dd, (int)dd, (int)rows, 0, 0, nullptr};
-      EpiBlend<TF, A> e{F, dd, 0, static_cast<A>(beta), static_cast<A>(alpha), vec_ok<TF>(F, dd, 0)};
-      return launch_gemm_qn<EpiBlend<TF, A>, true, true>(g, e, 1, stream, "gram_update");
-    }
-  }
   // X̃ᵀ, [dd][ldr], with the ones row appended and the token pad zeroed.
   if (launch_pack<TX, TX, A>(X, rows, d, d, 0, nullptr, nullptr, 0, 0, XT, ldr, 0, append_ones != 0, 1, stream))
     return -1;
@@ -154,8 +166,8 @@ size_t pto_gram_workspace_bytes(int x_dtype, int64_t rows, int64_t d, int append
 int pto_gram_update(void* F, int f_dtype, const void* X, int x_dtype, int64_t rows, int64_t d, int append_ones,
                     double beta, double alpha, void* workspace, size_t ws_bytes, void* stream) {
   PTO_REQUIRE(rows >= 0 && d >= 0, "gram_update_: negative extent");
-  PTO_REQUIRE((d == 0 && !append_ones) || (F && (rows == 0 || X) && workspace),
-              "gram_update_: null factor, input or workspace");
+  PTO_REQUIRE((d == 0 && !append_ones) || (F && (rows == 0 || X)), "gram_update_: null factor or input");
+  PTO_REQUIRE(workspace || ws_bytes == 0, "gram_update_: null workspace");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (x_dtype == pto::kBF16 && f_dtype == pto::kF32)
     return pto::gram_t<pto::bf16, float>(static_cast<float*>(F), static_cast<const pto::bf16*>(X), rows, d,

@@ -372,7 +372,7 @@ class HipBackend:
         x_work = X2.dtype if (X2.dtype == torch.bfloat16 and f_work == torch.float32) else f_work
         Fw = F if (F.dtype == f_work and F.is_contiguous()) else F.to(f_work).contiguous()
         Xw = X2.to(x_work).contiguous()
-        if _overlaps(Xw, Fw):
+        if _overlaps(Xw, Fw) or Xw.data_ptr() % 16:  # bf16 X may be read in place: 16-byte aligned
             Xw = Xw.clone()
         fc, xc = _DTYPE_CODE[f_work], _DTYPE_CODE[x_work]
         rows = Xw.shape[0]

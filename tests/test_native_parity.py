@@ -244,22 +244,51 @@ def test_gram_vs_oracle(native_backend, append_ones):
     assert _relfro(_np(F), want) <= 1e-6
 
 
-@pytest.mark.parametrize("rows, d", [(256, 200), (1024, 3000), (2048, 2048)])
-def test_gram_direct_transposing_reads_vs_oracle(native_backend, rows, d):
+@pytest.mark.parametrize("rows, d, direct", [(256, 200, True), (1024, 3000, True), (2048, 2048, True),
+                                             (1000, 200, False), (256, 204, False)])
+def test_gram_direct_transposing_reads_vs_oracle(native_backend, rows, d, direct):
     """bf16 X with a token count that is a multiple of 128, a width that is
     a multiple of 8 and no ones column is read in place as the transposing
     operand on both sides (128² tiles for d = 200 and 2048, 192² tiles with
-    a partial last tile row for d = 3000): EMA blend vs the oracle."""
+    a partial last tile row for d = 3000), with no workspace; a ragged token
+    count or width takes the packed Xᵀ path. Which one ran is read from the
+    library's per-kernel launch counts. EMA blend vs the oracle."""
+    be = ops._NATIVE
+    assert be._lib.pto_gram_workspace_bytes(2, rows, d, 0) == (0 if direct else 2 * d * ((rows + 127) // 128 * 128) + 512)
     g = torch.Generator(device="cpu").manual_seed(rows + d)
     X = torch.randn(rows, d, generator=g).bfloat16()
     F0 = torch.randn(d, d, generator=g)
     F0 = (F0 + F0.T) / 2
     F = F0.to(DEV)
-    ops.gram_update_(F, X.to(DEV), beta=0.9, alpha=0.1 / rows, append_ones=False)
+    Xd = X.to(DEV)
+    torch.cuda.synchronize()
+    be.prof_reset()
+    be.prof_enable(True)
+    try:
+        ops.gram_update_(F, Xd, beta=0.9, alpha=0.1 / rows, append_ones=False)
+        torch.cuda.synchronize()
+        counts = {k: be.prof_query(k)[1] for k in ("gram_update_direct", "gram_update")}
+    finally:
+        be.prof_enable(False)
+    assert counts == ({"gram_update_direct": 1, "gram_update": 0} if direct else
+                      {"gram_update_direct": 0, "gram_update": 1}), counts
     want = oo.gram_update(F0.numpy(), X.float().numpy(), 0.9, 0.1 / rows, False, dtype=np.float64)
     assert _relfro(_np(F), want) <= 1e-5
     Fs = _np(F)
     assert np.array_equal(Fs, Fs.T)
+
+
+def test_gram_direct_unaligned_input_is_copied(native_backend):
+    """A bf16 view that starts 2 bytes into its storage cannot be read in
+    place with 16-byte loads: the adapter copies it, the result is the same."""
+    g = torch.Generator(device="cpu").manual_seed(5)
+    X = torch.randn(256 * 64 + 1, generator=g).bfloat16()
+    Xv = X.to(DEV)[1:].view(256, 64)
+    assert Xv.data_ptr() % 16 != 0
+    F = torch.zeros(64, 64, device=DEV)
+    ops.gram_update_(F, Xv, beta=0.0, alpha=1.0, append_ones=False)
+    want = oo.gram_update(None, X[1:].view(256, 64).float().numpy(), 0.0, 1.0, False, dtype=np.float64)
+    assert _relfro(_np(F), want) <= 1e-5
 
 
 @pytest.mark.parametrize("d, append_ones", [(4000, True), (3900, False)])
