@@ -141,9 +141,16 @@ __global__ void root_init_kernel(const R* __restrict__ M, int64_t n, int64_t ld,
   }
 }
 
+// Error slots: each (iteration, matrix) maximum is spread over kErrSub
+// words, one per group of waves, and the decide kernel reduces them (one
+// word for every wave of a launch serialised thousands of atomics: 20-45 us
+// per iteration at n = 1024-2048).
+constexpr int kErrSub = 64;
+
 // Epilogue of Mk' = Mi^p·Mk (upper tiles + mirror): writes Mk' and the next
-// Mi and folds max|Mk' − I| into err[b * err_stride] (bitwise max of
-// non-negative values, which keeps NaN; err_stride 0 = one batch maximum).
+// Mi and folds max|Mk' − I| into err[b * err_stride + sub] (bitwise max of
+// non-negative values, which keeps NaN; err_stride 0 = one batch maximum;
+// sub spreads the waves over kErrSub words).
 template <typename R>
 struct EpiMk {
   typedef R S;
@@ -194,7 +201,8 @@ struct EpiMk {
       typename Bits<R>::U o = __shfl_xor(mx, off, 64);
       mx = o > mx ? o : mx;
     }
-    if ((threadIdx.x & 63) == 0) atomicMax(err + (int64_t)b * err_stride, mx);
+    const int sub = (int)((blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) & (kErrSub - 1));
+    if ((threadIdx.x & 63) == 0) atomicMax(err + (int64_t)b * err_stride + sub, mx);
   }
 };
 
@@ -213,13 +221,25 @@ __device__ void decide_one(RootState<R>& st, R e, int it, R tol) {
   }
 }
 
-// Global mode: one thread applies the rule to err[it]. Per-matrix mode: the
-// block applies it to each matrix (err[it·nb + b]) and then to the summary.
+// Maximum of one slot's kErrSub words (bit patterns of non-negative values).
+template <typename R>
+__device__ R err_slot_max(const R* slot) {
+  typedef typename Bits<R>::U U;
+  const U* w = reinterpret_cast<const U*>(slot);
+  U m = 0;
+  for (int j = 0; j < kErrSub; ++j) m = w[j] > m ? w[j] : m;
+  R r;
+  __builtin_memcpy(&r, &m, sizeof(R));
+  return r;
+}
+
+// Global mode: one thread applies the rule to slot it. Per-matrix mode: the
+// block applies it to each matrix (slot it·nb + b) and then to the summary.
 template <typename R>
 __global__ void __launch_bounds__(256) root_decide_kernel(RootState<R>* st, const R* __restrict__ err, int it, R tol,
                                                           int nb, int each) {
   if (!each) {
-    if (threadIdx.x == 0) decide_one(st[0], err[it], it, tol);
+    if (threadIdx.x == 0) decide_one(st[0], err_slot_max(err + (int64_t)it * kErrSub), it, tol);
     return;
   }
   __shared__ int live;
@@ -227,7 +247,7 @@ __global__ void __launch_bounds__(256) root_decide_kernel(RootState<R>* st, cons
   __syncthreads();
   int mine = 0;
   for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-    decide_one(st[1 + b], err[(int64_t)it * nb + b], it, tol);
+    decide_one(st[1 + b], err_slot_max(err + ((int64_t)it * nb + b) * kErrSub), it, tol);
     mine |= !st[1 + b].stopped;
   }
   if (mine) atomicOr(&live, 1);
@@ -274,7 +294,7 @@ size_t root_ws_bytes_t(int64_t batch, int64_t n, int64_t max_iter, bool each) {
   add(sizeof(double) * kRedBlocks * batch);
   add(sizeof(R) * batch);
   add(sizeof(R) * batch);
-  add(sizeof(R) * std::max<int64_t>(max_iter, 1) * (each ? batch : 1));
+  add(sizeof(R) * std::max<int64_t>(max_iter, 1) * (each ? batch : 1) * kErrSub);
   add(sizeof(RootState<R>) * (each ? 1 + batch : 1));
   for (int i = 0; i < kRootBufs; ++i) add(sizeof(R) * batch * n * ld);
   return bytes + 256;
@@ -297,7 +317,7 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   double* partial = cv.take<double>(kRedBlocks * batch);
   R* z = cv.take<R>(batch);
   R* xs = cv.take<R>(batch);
-  const int64_t n_err = std::max<int64_t>(max_iter, 1) * (each ? batch : 1);
+  const int64_t n_err = std::max<int64_t>(max_iter, 1) * (each ? batch : 1) * kErrSub;
   const int64_t n_st = each ? 1 + batch : 1;
   R* err = cv.take<R>(n_err);
   RootState<R>* st = cv.take<RootState<R>>(n_st);
@@ -420,8 +440,8 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     // Mk_{it+1} = S · Mk_it, with the fused next-Mi / error epilogue.
     {
       GemmArgs g{S, ld, sb, Mk[cur], ld, sb, (int)n, (int)n, (int)ld, 0, 0, guard, guard_stride};
-      EpiMk<R> e{Mk[nxt], Mi[nxt], ld, sb, c1, alpha, reinterpret_cast<U*>(err + (int64_t)it * (each ? nb : 1)),
-                 each ? 1 : 0, U(0), vec_ok<R>(Mk[nxt], ld, sb) && vec_ok<R>(Mi[nxt], ld, sb)};
+      EpiMk<R> e{Mk[nxt], Mi[nxt], ld, sb, c1, alpha,
+                 reinterpret_cast<U*>(err + (int64_t)it * (each ? nb : 1) * kErrSub), each ? kErrSub : 0, U(0), vec_ok<R>(Mk[nxt], ld, sb) && vec_ok<R>(Mi[nxt], ld, sb)};
       if (launch_gemm<R, true, EpiMk<R>, true>(g, e, nb, stream, "root_mk")) return -1;
     }
     hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(each ? 256 : 64), 0, stream, st, err, it,
