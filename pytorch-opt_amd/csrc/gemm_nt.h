@@ -1,9 +1,10 @@
-// MFMA "NT" product core for gfx950:  C[b](i,j) = sum_k P[b](i,k) * Q[b](j,k)
+// MFMA product core for gfx950:  C[b](i,j) = sum_k P[b](i,k) * Q[b](j,k)
 //
-// Both operands are row-major with K contiguous, which is the layout every
-// product on the pytorch_opt.ops path can be put into (X·Xᵀ, S·S for
-// symmetric S, B·X via a stored Xᵀ, ...). That keeps each lane's MFMA
-// fragment a contiguous 16-byte run in LDS for all three element types.
+// Operands are row-major with K contiguous ("NT", every element type: X·Xᵀ,
+// S·S for symmetric S, B·X via a stored Xᵀ, ...), where each lane's MFMA
+// fragment is a contiguous 16-byte run in LDS; bf16 operands may instead be
+// stored [K][·] ("QN" for Q, "PT" for P) and read through transposing LDS
+// loads (see below).
 //
 // Operand contract (checked by the host launchers):
 //   * K is a multiple of one ring of K tiles (Tile::NS * BK) and the pad

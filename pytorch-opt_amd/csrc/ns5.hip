@@ -10,14 +10,19 @@
 // Per iteration three MFMA launches, each with a fused epilogue:
 //   1. A = X·Xᵀ                    symmetric: upper tiles only, mirrored store
 //   2. B' = a·I + b·A + c·(A·A)    symmetric: upper tiles only, mirrored store
-//   3. X' = B'·X  (= a·X + B·X)    full; writes X' and X'ᵀ (Xᵀ is the
-//                                  K-major operand the next product needs)
+//   3. X' = B'·X  (= a·X + B·X)    full
 // Folding a·X into the product as a·I on the diagonal of B' spares the
 // update a read of X; the extra rounding is that of one bf16 store of
 // a + B_ii, the same size as the rounding of a·X itself in a bf16 chain.
-// All three are "NT" products over K-contiguous rows. bf16 inputs keep
-// X, A, B in bf16 between launches with fp32 accumulation; fp32 and fp64
-// inputs stay in their own precision throughout.
+// Layouts: the gram reads X's K-contiguous rows on both sides ("NT"). In
+// bf16 the square and the update read their operands from [K][·] arrays
+// through transposing LDS loads (A and B' are symmetric, so each is its own
+// transpose; X' = B'·X reads X as stored), so X is kept in one layout; the
+// first iteration reads a caller's 128-aligned bf16 G in place, with the
+// 1/(‖G‖+eps) scale applied in the gram's and update's epilogues. In fp32
+// and fp64 the update reads a stored Xᵀ, which its epilogue writes beside
+// X'. bf16 inputs keep X, A, B in bf16 between launches with fp32
+// accumulation; fp32 and fp64 inputs stay in their own precision.
 #include <algorithm>
 #include <mutex>
 #include <string>
