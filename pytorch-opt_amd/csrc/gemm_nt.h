@@ -18,9 +18,10 @@
 // for (i, j), i <= j, is stored at (i, j) and at (j, i), so the result is an
 // exactly symmetric matrix at half the MFMA work.
 //
-// Pipeline: a ring of LDS stages (four, or eight for the small fp32/fp64
-// tiles) filled by direct global-to-LDS loads, NS - 1 K tiles ahead of the
-// MFMAs; one barrier per K tile (details below).
+// Pipeline: a ring of LDS stages (four, or eight for the small fp32 tiles)
+// filled by direct global-to-LDS loads, NS - 1 K tiles ahead of the MFMAs;
+// one barrier per K tile, or two in the ping-pong schedule of the 256² bf16
+// tiles (details below).
 #pragma once
 
 #include <atomic>
@@ -166,8 +167,9 @@ __device__ __forceinline__ void decode_tile(int t, int tiles_m, int tiles_n, int
 //
 // A tile's load is issued NS - 2 steps before its LDS reads, so a step
 // cannot be shorter than the load latency / (NS - 2). The big tiles' steps
-// (512+ MFMA cycles per wave) cover it with four stages; the small fp32 and
-// fp64 tiles (128-512 cycles per step) use eight.
+// (512+ MFMA cycles per wave) cover it with four stages; the small fp32
+// tiles (128-512 cycles per step) use eight (measured a few percent faster
+// on one-matrix roots, where their launches are latency-bound).
 //
 // LDS rows are unpadded; 16-byte chunk c of row r lives at physical chunk
 // c ^ f(r), f(r) = ((r >> 2) & 3) ^ (r & 2), which makes the fragment
