@@ -25,6 +25,7 @@
 #pragma once
 
 #include <atomic>
+#include <type_traits>
 
 #include "pto_common.h"
 
@@ -97,14 +98,17 @@ struct Mfma<double> {  // v_mfma_f64_16x16x4_f64
 };
 
 // Tile configuration: BM x BN output tile, BK deep (64 bytes), WM x WN
-// waves, NS LDS stages (4 or 8), PP: ping-pong schedule (main loop).
-template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_ = 4, bool PP_ = false>
+// waves, NS LDS stages (4 or 8), PP: ping-pong schedule (main loop), KG:
+// K groups (KG = 2: two WM x WN wave groups take alternate K tiles, each
+// accumulating the whole tile, summed at the end).
+template <int BM_, int BN_, int BK_, int WM_, int WN_, int NS_ = 4, bool PP_ = false, int KG_ = 1>
 struct Tile {
-  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_, NS = NS_, KG = KG_;
   static constexpr bool PP = PP_;
-  static constexpr int NT = 64 * WM * WN;
+  static constexpr int NT = 64 * WM * WN * KG;
   static_assert(NS == 4 || NS == 8, "ring of 4 or 8 stages");
-  static_assert(!PP || (NS == 4 && WM == 2 && WN == 4), "ping-pong: two groups of four waves, four stages");
+  static_assert(!PP || (NS == 4 && WM == 2 && WN == 4 && KG == 1), "ping-pong: two groups of four waves, four stages");
+  static_assert(KG == 1 || (KG == 2 && NS == 4 && !PP), "K groups: two, four stages");
 };
 
 struct GemmArgs {
@@ -232,21 +236,23 @@ typedef __attribute__((address_space(1))) const void gbl_void_t;
 
 // LDS plan: NS stages of (BM + BN) rows x 64 bytes; after the loop each
 // stage array also hosts the epilogue staging of WPA waves (RPP rows x
-// (WTN + 1) accumulator-type values per wave, odd pitch).
+// (WTN + 1) accumulator-type values per wave, odd pitch). With K groups a
+// wave stores WTE = WTM / KG rows of its sub-tile (the partner group stores
+// the rest).
 template <typename T, class Cfg, typename S>
 struct LdsPlan {
-  static constexpr int NW = Cfg::WM * Cfg::WN, NS = Cfg::NS;
-  static constexpr int WTM = Cfg::BM / Cfg::WM, WTN = Cfg::BN / Cfg::WN;
+  static constexpr int NW = Cfg::WM * Cfg::WN * Cfg::KG, NS = Cfg::NS;
+  static constexpr int WTM = Cfg::BM / Cfg::WM, WTN = Cfg::BN / Cfg::WN, WTE = WTM / Cfg::KG;
   static constexpr int STAGE = (Cfg::BM + Cfg::BN) * kRowBytes;
   static constexpr int WPA = (NW + NS - 1) / NS;  // waves per array in the epilogue
   static constexpr int SP = WTN + 1;
   static constexpr int kLdsMax = 160 * 1024;
   // rows per epilogue pass: the largest multiple of 16, at most 64, that
-  // divides the wave tile's rows and lets the four arrays fit
+  // divides the rows a wave stores and lets the four arrays fit
   static constexpr int pick_rpp() {
-    for (int r = (WTM < 64 ? WTM : 64) / 16 * 16; r > 16; r -= 16) {
+    for (int r = (WTE < 64 ? WTE : 64) / 16 * 16; r > 16; r -= 16) {
       const int epi = WPA * r * SP * (int)sizeof(S);
-      if (WTM % r == 0 && NS * (STAGE > epi ? STAGE : epi) <= kLdsMax) return r;
+      if (WTE % r == 0 && NS * (STAGE > epi ? STAGE : epi) <= kLdsMax) return r;
     }
     return 16;
   }
@@ -285,7 +291,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   static_assert(KSPAN % VEC == 0 && NRG >= 1, "fragment runs");
   constexpr int NS = Cfg::NS;
   static_assert((NS - 2) * IPW <= 63, "vmcnt range");
-  static_assert(Plan::RPP % MF::MN == 0 && WTM % Plan::RPP == 0, "epilogue passes");
+  static_assert(Plan::RPP % MF::MN == 0 && Plan::WTE % Plan::RPP == 0, "epilogue passes");
+  constexpr int KG = Cfg::KG, NWG = Cfg::WM * Cfg::WN;  // K groups, waves per group
+  static_assert(KG == 1 || (FM % 2 == 0 && Plan::WTE % MF::MN == 0), "K groups: halves of whole fragments");
   static_assert(Cfg::NS * Plan::ARR <= Plan::kLdsMax, "LDS budget");
   static_assert(!QN || (sizeof(T) == 2 && (!UPPER || PT) && CPR >= 16 && (QRB % 256 == 0 || QRB % 256 == 128) &&
                         (BM * kRowBytes) % 1024 == 0 && NRG == 1),
@@ -306,7 +314,8 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // wave index in a scalar register: DMA destinations and per-wave offsets
   // are then scalar arithmetic
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
+  const int kg = wave / NWG, wl = wave - kg * NWG;  // K group, wave in the group
+  const int wm = wl / Cfg::WN, wn = wl % Cfg::WN;
   const int ntile = gridDim.x;  // tiles per matrix
   const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y);
   const int b = logical / ntile;
@@ -502,7 +511,66 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // every step of the unrolled group is a real one and the MFMAs need no
   // branch.
   const int KT = g.K / BK;
-  if constexpr (Cfg::PP) {
+  if constexpr (KG == 2) {
+    // K groups: waves 0..NWG-1 (group 0) take the even K tiles, the others
+    // the odd ones, each group accumulating the whole tile in its own
+    // registers (summed after the loop). Intervals j = 0 .. KT, each ended
+    // by lgkmcnt(0), vmcnt(2·IPW) and a barrier: in interval j the group of
+    // tile j reads it (R) into its one register set while the other group
+    // issues the MFMAs of tile j-1 (M), and every wave issues its share of
+    // the DMA of tile j+3 into the stage of tile j-1 (read in interval j-1).
+    // vmcnt(2·IPW) leaves only tiles j+2, j+3 in flight, so tile j+1 has
+    // landed when interval j+1 reads it. Per group this is R, M, R, M, ...
+    // over its own tiles, group 1 starting one interval late and group 0
+    // ending one late, so both run KT + 1 intervals.
+    if (KT > 0) {
+      Frag f;
+      issue(0, st0);
+      issue(min(1, KT - 1), st1);
+      issue(min(2, KT - 1), st2);
+      __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));
+      stage_barrier();
+#define PTO_KG_END()                                          \
+  __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));             \
+  __builtin_amdgcn_sched_barrier(0);                          \
+  stage_barrier();                                            \
+  __builtin_amdgcn_sched_barrier(0);
+#define PTO_KG_R(J, RD, DMA)                                  \
+  load_frags(RD, f);                                          \
+  issue(min((J) + 3, KT - 1), DMA);                           \
+  PTO_KG_END()
+#define PTO_KG_M(J, DMA)                                      \
+  mma(f);                                                     \
+  issue(min((J) + 3, KT - 1), DMA);                           \
+  PTO_KG_END()
+      if (kg == 0) {
+        // tiles 4v and 4v+2: intervals 4v .. 4v+3
+        for (int v = 0; v < KT; v += kStages) {
+          PTO_KG_R(v, st0, st3)
+          PTO_KG_M(v + 1, st0)
+          PTO_KG_R(v + 2, st2, st1)
+          PTO_KG_M(v + 3, st2)
+        }
+        issue(KT - 1, st3);  // interval KT (tile KT-1 is group 1's)
+        PTO_KG_END()
+      } else {
+        issue(min(3, KT - 1), st3);  // interval 0 (tile 0 is group 0's)
+        PTO_KG_END()
+        // tiles 4v+1 and 4v+3: intervals 4v+1 .. 4v+4
+        for (int v = 0; v < KT; v += kStages) {
+          PTO_KG_R(v + 1, st1, st0)
+          PTO_KG_M(v + 2, st1)
+          PTO_KG_R(v + 3, st3, st2)
+          PTO_KG_M(v + 4, st3)
+        }
+      }
+#undef PTO_KG_R
+#undef PTO_KG_M
+#undef PTO_KG_END
+      __builtin_amdgcn_s_waitcnt(PTO_VMCNT(0));
+      stage_barrier();
+    }
+  } else if constexpr (Cfg::PP) {
     // Ping-pong: waves 0-3 (group 0) and 4-7 (group 1), one of each per
     // SIMD, run the same sequence of phases, group 1 one phase behind:
     //   R(t): LDS reads of tile t into the one register set, DMA of tile
@@ -626,7 +694,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // at (i, j) by its own direct pass and at (j, i) by its transposed pass;
   // on diagonal tiles positions below the diagonal are skipped by the
   // direct pass, so the stored matrix is exactly symmetric.
-  constexpr int RPP = Plan::RPP, SP = Plan::SP;
+  constexpr int RPP = Plan::RPP, SP = Plan::SP, WTE = Plan::WTE;
   const int wa = wave / Plan::WPA;  // < NS
   char* arr = wa == 0 ? st0 : wa == 1 ? st1 : wa == 2 ? st2 : wa == 3 ? st3 : wa == 4 ? st4 : wa == 5 ? st5 : wa == 6 ? st6 : st7;
   S* stg = reinterpret_cast<S*>(arr) + (wave % Plan::WPA) * RPP * SP;
@@ -648,82 +716,131 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // transposed runs: 8 lanes share a column c and cover 64 consecutive rows
   constexpr int CBT = WTN / 8;
   constexpr int ITEMS_T = ((RPP / 8 + 7) / 8) * CBT;
+  if constexpr (KG == 2) {
+    // Sum the two groups' partial tiles: each wave keeps WTE rows of its
+    // sub-tile (group 0 the first half, group 1 the second) and hands the
+    // other half to its partner (same wm, wn, other group) through LDS,
+    // 16 bytes per lane per fragment, lane-minor (each instruction writes
+    // one contiguous KiB). Every wave adds the other group's values to its
+    // own, so both halves hold (even tiles) + (odd tiles).
+    constexpr int HF = FM / 2, PER = HF * FN;
+    static_assert(sizeof(cvec_t) == 16 && NW <= 2 * NS && 2 * PER * 1024 <= Plan::ARR,
+                  "K-group exchange: 4-byte accumulators, two waves per stage array");
+    auto slot = [&](int w) -> char* {
+      const int a = w / 2;
+      char* base = a == 0 ? st0 : a == 1 ? st1 : a == 2 ? st2 : st3;
+      return base + (w & 1) * (PER * 1024);
+    };
+    auto exchange = [&](auto send_c, auto keep_c) {
+      constexpr int SEND = decltype(send_c)::value, KEEP = decltype(keep_c)::value;
+      char* mine = slot(wave);
 #pragma unroll
-  for (int hp = 0; hp < WTM / RPP; ++hp) {
-    const int pr0 = wr0 + hp * RPP;  // first output row of this pass
-    if (pr0 >= g.M || nrem <= 0) break;
-    const int rows = min(RPP, g.M - pr0);
-    typename Epi::Pre pre[ITEMS];
+      for (int e = 0; e < PER; ++e)
+        *reinterpret_cast<cvec_t*>(mine + (e * 64 + lane) * 16) = acc[SEND + e / FN][e % FN];
+      stage_barrier();
+      const char* theirs = slot(kg ? wave - NWG : wave + NWG);
 #pragma unroll
-    for (int it = 0; it < ITEMS; ++it) {
-      const int r = (it / CBLK) * RPB + lane / LGD;
-      const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
-      const int i = pr0 + r, j0 = wc0 + c;
-      const int n = min(8, nrem - c);
-      const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
-      if (lane_ok && r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);
-    }
+      for (int e = 0; e < PER; ++e) {
+        const cvec_t o = *reinterpret_cast<const cvec_t*>(theirs + (e * 64 + lane) * 16);
 #pragma unroll
-    for (int fm = hp * (RPP / MF::MN); fm < (hp + 1) * (RPP / MF::MN); ++fm)
+        for (int r = 0; r < MF::NACC; ++r) acc[KEEP + e / FN][e % FN][r] += o[r];
+      }
+      stage_barrier();  // the arrays host the epilogue staging next
+    };
+    if (kg == 0)
+      exchange(std::integral_constant<int, HF>{}, std::integral_constant<int, 0>{});
+    else
+      exchange(std::integral_constant<int, 0>{}, std::integral_constant<int, HF>{});
+  }
+  // EFM: the first fragment row this wave stores (its sub-tile's, or with K
+  // groups its half's), a constant so that acc stays in registers
+  auto store_rows = [&](auto efm_c) {
+    constexpr int EFM = decltype(efm_c)::value;
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn)
+    for (int hp = 0; hp < WTE / RPP; ++hp) {
+      const int pr0 = wr0 + EFM * MF::MN + hp * RPP;  // first output row of this pass
+      if (pr0 >= g.M || nrem <= 0) break;
+      const int rows = min(RPP, g.M - pr0);
+      typename Epi::Pre pre[ITEMS];
 #pragma unroll
-        for (int r = 0; r < MF::NACC; ++r) {
-          const int li = fm * MF::MN - hp * RPP + MF::row(lane, r);
-          const int lj = fn * MF::MN + MF::col(lane, r);
-          stg[li * SP + lj] = static_cast<S>(acc[fm][fn][r]);
+      for (int it = 0; it < ITEMS; ++it) {
+        const int r = (it / CBLK) * RPB + lane / LGD;
+        const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
+        const int i = pr0 + r, j0 = wc0 + c;
+        const int n = min(8, nrem - c);
+        const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
+        if (lane_ok && r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);
+      }
+#pragma unroll
+      for (int fm = EFM + hp * (RPP / MF::MN); fm < EFM + (hp + 1) * (RPP / MF::MN); ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int r = 0; r < MF::NACC; ++r) {
+            const int li = (fm - EFM) * MF::MN - hp * RPP + MF::row(lane, r);
+            const int lj = fn * MF::MN + MF::col(lane, r);
+            stg[li * SP + lj] = static_cast<S>(acc[fm][fn][r]);
+          }
+      __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int it = 0; it < ITEMS; ++it) {
+        const int r = (it / CBLK) * RPB + lane / LGD;
+        const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
+        const int i = pr0 + r, j0 = wc0 + c;
+        const int n = min(8, nrem - c);
+        const int kbeg = diag ? max(0, i - j0) : 0;
+        if (!(lane_ok && r < rows && c < nrem && kbeg < n)) continue;
+        S v[8], vo[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
+        epi.put(b, i, j0, v, kbeg, n, pre[it], vo);
+        if (need_t && !Epi::kVoIsV) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];
         }
-    __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int it = 0; it < ITEMS; ++it) {
-      const int r = (it / CBLK) * RPB + lane / LGD;
-      const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
-      const int i = pr0 + r, j0 = wc0 + c;
-      const int n = min(8, nrem - c);
-      const int kbeg = diag ? max(0, i - j0) : 0;
-      if (!(lane_ok && r < rows && c < nrem && kbeg < n)) continue;
-      S v[8], vo[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
-      epi.put(b, i, j0, v, kbeg, n, pre[it], vo);
-      if (need_t && !Epi::kVoIsV) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];
       }
+      if (need_t) {
+        if constexpr (!Epi::kVoIsV) {  // the write-back above must land first
+          __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+          __builtin_amdgcn_wave_barrier();
+        }
+        // output row j = wc0 + c, columns i = pr0 + r..r+7
+        typename Epi::PreT pret[ITEMS_T];
+#pragma unroll
+        for (int it = 0; it < ITEMS_T; ++it) {
+          const int c = (it % CBT) * 8 + lane / 8;
+          const int r = ((it / CBT) * 8 + lane % 8) * 8;
+          const int j = wc0 + c, i0 = pr0 + r;
+          int n = min(8, rows - r);
+          if (diag) n = min(n, j - i0);  // strictly below the diagonal
+          if (c < nrem && r < rows && n > 0) epi.load_t(b, j, i0, n, pret[it]);
+        }
+#pragma unroll
+        for (int it = 0; it < ITEMS_T; ++it) {
+          const int c = (it % CBT) * 8 + lane / 8;
+          const int r = ((it / CBT) * 8 + lane % 8) * 8;
+          const int j = wc0 + c, i0 = pr0 + r;
+          int n = min(8, rows - r);
+          if (diag) n = min(n, j - i0);
+          if (!(c < nrem && r < rows && n > 0)) continue;
+          S v[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(r + k) * SP + c] : S(0);
+          epi.put_t(b, j, i0, v, n, pret[it]);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
+      __builtin_amdgcn_wave_barrier();
     }
-    if (need_t) {
-      if constexpr (!Epi::kVoIsV) {  // the write-back above must land first
-        __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-        __builtin_amdgcn_wave_barrier();
-      }
-      // output row j = wc0 + c, columns i = pr0 + r..r+7
-      typename Epi::PreT pret[ITEMS_T];
-#pragma unroll
-      for (int it = 0; it < ITEMS_T; ++it) {
-        const int c = (it % CBT) * 8 + lane / 8;
-        const int r = ((it / CBT) * 8 + lane % 8) * 8;
-        const int j = wc0 + c, i0 = pr0 + r;
-        int n = min(8, rows - r);
-        if (diag) n = min(n, j - i0);  // strictly below the diagonal
-        if (c < nrem && r < rows && n > 0) epi.load_t(b, j, i0, n, pret[it]);
-      }
-#pragma unroll
-      for (int it = 0; it < ITEMS_T; ++it) {
-        const int c = (it % CBT) * 8 + lane / 8;
-        const int r = ((it / CBT) * 8 + lane % 8) * 8;
-        const int j = wc0 + c, i0 = pr0 + r;
-        int n = min(8, rows - r);
-        if (diag) n = min(n, j - i0);
-        if (!(c < nrem && r < rows && n > 0)) continue;
-        S v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(r + k) * SP + c] : S(0);
-        epi.put_t(b, j, i0, v, n, pret[it]);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-    __builtin_amdgcn_wave_barrier();
+  };
+  if constexpr (KG == 1) {
+    store_rows(std::integral_constant<int, 0>{});
+  } else {
+    if (kg == 0)
+      store_rows(std::integral_constant<int, 0>{});
+    else
+      store_rows(std::integral_constant<int, FM / 2>{});
   }
   epi.finish(b);
 }
@@ -749,7 +866,9 @@ struct TileSet<bf16> {
   typedef Tile<128, 128, 32, 2, 2> small;
   typedef Tile<256, 256, 32, 2, 4, 4, true> sym_big;
   typedef Tile<128, 128, 32, 2, 2> sym_small;
-  typedef Tile<192, 192, 32, 2, 4> sym_mid;
+  // the 192² tile: two K groups of four 96×96 waves (LDS bytes per MFMA
+  // as the 256² tile's; K-FAC Gram and one-matrix NS5 products −1–5%)
+  typedef Tile<192, 192, 32, 2, 2, 4, false, 2> sym_mid;
   typedef sym_small sym_tiny;  // unused
   static constexpr bool kHasMid = true, kHasTiny = false;
   static constexpr double kBigRate = 1.5;

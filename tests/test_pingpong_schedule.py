@@ -1,4 +1,5 @@
-"""CPU model of the MFMA core's ping-pong main loop (the 256² bf16 tiles).
+"""CPU models of the MFMA core's two-group main loops: the ping-pong schedule
+(the 256² bf16 tiles) and the K-group schedule (the 192² bf16 tile).
 
 The kernel splits its eight waves into two groups of four (one wave of each
 per SIMD). Each wave runs the same phases over K tiles t = 0, 1, ...:
@@ -43,7 +44,10 @@ def _phases(group, KT, stages=4, wait_keep=2, g1_extra=True):
 
 
 def _check(KT, **kw):
-    seqs = {g: _phases(g, KT, **kw) for g in (0, 1)}
+    return _check_seqs({g: _phases(g, KT, **kw) for g in (0, 1)}, KT)
+
+
+def _check_seqs(seqs, KT):
     if len(seqs[0]) != len(seqs[1]):
         raise AssertionError(f"barrier counts differ: {len(seqs[0])} vs {len(seqs[1])}")
     issued = {0: [], 1: []}   # per group: [tile, stage, phase, landed-by-phase or None]
@@ -88,3 +92,41 @@ def test_pingpong_schedule_is_hazard_free(KT):
 def test_pingpong_planted_mistakes_are_caught(planted):
     with pytest.raises(AssertionError):
         _check(16, **planted)
+
+
+def _kgroup_phases(group, KT, stages=4, wait_keep=2, late_start=True):
+    """K groups: group g reads and multiplies the K tiles t with t % 2 == g;
+    interval j: the reader of tile j reads it, the other group multiplies
+    tile j - 1, every wave issues its DMA share of tile j + 3 into stage
+    (j + 3) % 4; group 1 starts with an interval of DMA only, group 0 ends
+    with one."""
+    ph = [[("dma", t, t % stages) for t in range(min(stages - 1, 3))] + [("wait", wait_keep)]]
+    j = 0
+    if group == 1 and late_start:
+        ph.append([("dma", min(3, KT - 1), 3 % stages), ("wait", wait_keep)])
+        j = 1
+    for t in range(group, KT, 2):  # (without the late start, group 1 runs one interval early)
+        ph.append([("read", t, t % stages), ("dma", min(j + 3, KT - 1), (j + 3) % stages), ("wait", wait_keep)])
+        j += 1
+        ph.append([("mma", t), ("dma", min(j + 3, KT - 1), (j + 3) % stages), ("wait", wait_keep)])
+        j += 1
+    if group == 0:
+        ph.append([("dma", min(j + 3, KT - 1), (j + 3) % stages), ("wait", wait_keep)])
+    ph.append([("wait", 0)])
+    return ph
+
+
+def _check_kgroup(KT, **kw):
+    seqs = {g: _kgroup_phases(g, KT, **kw) for g in (0, 1)}
+    return _check_seqs(seqs, KT)
+
+
+@pytest.mark.parametrize("KT", [4, 8, 12, 64, 512])
+def test_kgroup_schedule_is_hazard_free(KT):
+    assert _check_kgroup(KT) == KT + 3
+
+
+@pytest.mark.parametrize("planted", [dict(late_start=False), dict(stages=3), dict(wait_keep=3)])
+def test_kgroup_planted_mistakes_are_caught(planted):
+    with pytest.raises(AssertionError):
+        _check_kgroup(16, **planted)
