@@ -314,7 +314,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // wave index in a scalar register: DMA destinations and per-wave offsets
   // are then scalar arithmetic
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kg = wave / NWG, wl = wave - kg * NWG;  // K group, wave in the group
+  const int kg = KG == 1 ? 0 : wave / NWG, wl = wave - kg * NWG;  // K group, wave in the group
   const int wm = wl / Cfg::WN, wn = wl % Cfg::WN;
   const int ntile = gridDim.x;  // tiles per matrix
   const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y);
@@ -752,96 +752,97 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     else
       exchange(std::integral_constant<int, 0>{}, std::integral_constant<int, HF>{});
   }
-  // EFM: the first fragment row this wave stores (its sub-tile's, or with K
-  // groups its half's), a constant so that acc stays in registers
-  auto store_rows = [&](auto efm_c) {
-    constexpr int EFM = decltype(efm_c)::value;
-#pragma unroll
-    for (int hp = 0; hp < WTE / RPP; ++hp) {
-      const int pr0 = wr0 + EFM * MF::MN + hp * RPP;  // first output row of this pass
-      if (pr0 >= g.M || nrem <= 0) break;
-      const int rows = min(RPP, g.M - pr0);
-      typename Epi::Pre pre[ITEMS];
-#pragma unroll
-      for (int it = 0; it < ITEMS; ++it) {
-        const int r = (it / CBLK) * RPB + lane / LGD;
-        const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
-        const int i = pr0 + r, j0 = wc0 + c;
-        const int n = min(8, nrem - c);
-        const int kbeg = diag ? max(0, i - j0) : 0;  // skip i > j on diagonal tiles
-        if (lane_ok && r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);
-      }
-#pragma unroll
-      for (int fm = EFM + hp * (RPP / MF::MN); fm < EFM + (hp + 1) * (RPP / MF::MN); ++fm)
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-          for (int r = 0; r < MF::NACC; ++r) {
-            const int li = (fm - EFM) * MF::MN - hp * RPP + MF::row(lane, r);
-            const int lj = fn * MF::MN + MF::col(lane, r);
-            stg[li * SP + lj] = static_cast<S>(acc[fm][fn][r]);
-          }
-      __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int it = 0; it < ITEMS; ++it) {
-        const int r = (it / CBLK) * RPB + lane / LGD;
-        const int c = ((it % CBLK) * LGD + lane % LGD) * 8;
-        const int i = pr0 + r, j0 = wc0 + c;
-        const int n = min(8, nrem - c);
-        const int kbeg = diag ? max(0, i - j0) : 0;
-        if (!(lane_ok && r < rows && c < nrem && kbeg < n)) continue;
-        S v[8], vo[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];
-        epi.put(b, i, j0, v, kbeg, n, pre[it], vo);
-        if (need_t && !Epi::kVoIsV) {
-#pragma unroll
-          for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];
-        }
-      }
-      if (need_t) {
-        if constexpr (!Epi::kVoIsV) {  // the write-back above must land first
-          __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-          __builtin_amdgcn_wave_barrier();
-        }
-        // output row j = wc0 + c, columns i = pr0 + r..r+7
-        typename Epi::PreT pret[ITEMS_T];
-#pragma unroll
-        for (int it = 0; it < ITEMS_T; ++it) {
-          const int c = (it % CBT) * 8 + lane / 8;
-          const int r = ((it / CBT) * 8 + lane % 8) * 8;
-          const int j = wc0 + c, i0 = pr0 + r;
-          int n = min(8, rows - r);
-          if (diag) n = min(n, j - i0);  // strictly below the diagonal
-          if (c < nrem && r < rows && n > 0) epi.load_t(b, j, i0, n, pret[it]);
-        }
-#pragma unroll
-        for (int it = 0; it < ITEMS_T; ++it) {
-          const int c = (it % CBT) * 8 + lane / 8;
-          const int r = ((it / CBT) * 8 + lane % 8) * 8;
-          const int j = wc0 + c, i0 = pr0 + r;
-          int n = min(8, rows - r);
-          if (diag) n = min(n, j - i0);
-          if (!(c < nrem && r < rows && n > 0)) continue;
-          S v[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(r + k) * SP + c] : S(0);
-          epi.put_t(b, j, i0, v, n, pret[it]);
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(PTO_LGKM0);
-      __builtin_amdgcn_wave_barrier();
-    }
-  };
-  if constexpr (KG == 1) {
-    store_rows(std::integral_constant<int, 0>{});
-  } else {
-    if (kg == 0)
-      store_rows(std::integral_constant<int, 0>{});
-    else
-      store_rows(std::integral_constant<int, FM / 2>{});
+  // The epilogue for the fragment rows EFM .. EFM + WTE/16 - 1 of this
+  // wave's sub-tile (all of them, or with K groups its half), written
+  // out with a constant EFM so that acc stays in registers.
+#define PTO_STORE_ROWS(EFM)                                                                          \
+_Pragma("unroll")                                                                                    \
+  for (int hp = 0; hp < WTE / RPP; ++hp) {                                                           \
+    const int pr0 = wr0 + (EFM) * MF::MN + hp * RPP;  /* first output row of this pass */            \
+    if (pr0 >= g.M || nrem <= 0) break;                                                              \
+    const int rows = min(RPP, g.M - pr0);                                                            \
+    typename Epi::Pre pre[ITEMS];                                                                    \
+_Pragma("unroll")                                                                                    \
+    for (int it = 0; it < ITEMS; ++it) {                                                             \
+      const int r = (it / CBLK) * RPB + lane / LGD;                                                  \
+      const int c = ((it % CBLK) * LGD + lane % LGD) * 8;                                            \
+      const int i = pr0 + r, j0 = wc0 + c;                                                           \
+      const int n = min(8, nrem - c);                                                                \
+      const int kbeg = diag ? max(0, i - j0) : 0;  /* skip i > j on diagonal tiles */                \
+      if (lane_ok && r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);         \
+    }                                                                                                \
+_Pragma("unroll")                                                                                    \
+    for (int fm = (EFM) + hp * (RPP / MF::MN); fm < (EFM) + (hp + 1) * (RPP / MF::MN); ++fm)         \
+_Pragma("unroll")                                                                                    \
+      for (int fn = 0; fn < FN; ++fn)                                                                \
+_Pragma("unroll")                                                                                    \
+        for (int r = 0; r < MF::NACC; ++r) {                                                         \
+          const int li = (fm - (EFM)) * MF::MN - hp * RPP + MF::row(lane, r);                        \
+          const int lj = fn * MF::MN + MF::col(lane, r);                                             \
+          stg[li * SP + lj] = static_cast<S>(acc[fm][fn][r]);                                        \
+        }                                                                                            \
+    __builtin_amdgcn_s_waitcnt(PTO_LGKM0);                                                           \
+    __builtin_amdgcn_wave_barrier();                                                                 \
+_Pragma("unroll")                                                                                    \
+    for (int it = 0; it < ITEMS; ++it) {                                                             \
+      const int r = (it / CBLK) * RPB + lane / LGD;                                                  \
+      const int c = ((it % CBLK) * LGD + lane % LGD) * 8;                                            \
+      const int i = pr0 + r, j0 = wc0 + c;                                                           \
+      const int n = min(8, nrem - c);                                                                \
+      const int kbeg = diag ? max(0, i - j0) : 0;                                                    \
+      if (!(lane_ok && r < rows && c < nrem && kbeg < n)) continue;                                  \
+      S v[8], vo[8];                                                                                 \
+_Pragma("unroll")                                                                                    \
+      for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];                                        \
+      epi.put(b, i, j0, v, kbeg, n, pre[it], vo);                                                    \
+      if (need_t && !Epi::kVoIsV) {                                                                  \
+_Pragma("unroll")                                                                                    \
+        for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];                                     \
+      }                                                                                              \
+    }                                                                                                \
+    if (need_t) {                                                                                    \
+      if constexpr (!Epi::kVoIsV) {  /* the write-back above must land first */                      \
+        __builtin_amdgcn_s_waitcnt(PTO_LGKM0);                                                       \
+        __builtin_amdgcn_wave_barrier();                                                             \
+      }                                                                                              \
+  /* output row j = wc0 + c, columns i = pr0 + r..r+7 */                                             \
+      typename Epi::PreT pret[ITEMS_T];                                                              \
+_Pragma("unroll")                                                                                    \
+      for (int it = 0; it < ITEMS_T; ++it) {                                                         \
+        const int c = (it % CBT) * 8 + lane / 8;                                                     \
+        const int r = ((it / CBT) * 8 + lane % 8) * 8;                                               \
+        const int j = wc0 + c, i0 = pr0 + r;                                                         \
+        int n = min(8, rows - r);                                                                    \
+        if (diag) n = min(n, j - i0);  /* strictly below the diagonal */                             \
+        if (c < nrem && r < rows && n > 0) epi.load_t(b, j, i0, n, pret[it]);                        \
+      }                                                                                              \
+_Pragma("unroll")                                                                                    \
+      for (int it = 0; it < ITEMS_T; ++it) {                                                         \
+        const int c = (it % CBT) * 8 + lane / 8;                                                     \
+        const int r = ((it / CBT) * 8 + lane % 8) * 8;                                               \
+        const int j = wc0 + c, i0 = pr0 + r;                                                         \
+        int n = min(8, rows - r);                                                                    \
+        if (diag) n = min(n, j - i0);                                                                \
+        if (!(c < nrem && r < rows && n > 0)) continue;                                              \
+        S v[8];                                                                                      \
+_Pragma("unroll")                                                                                    \
+        for (int k = 0; k < 8; ++k) v[k] = k < n ? stg[(r + k) * SP + c] : S(0);                     \
+        epi.put_t(b, j, i0, v, n, pret[it]);                                                         \
+      }                                                                                              \
+    }                                                                                                \
+    __builtin_amdgcn_s_waitcnt(PTO_LGKM0);                                                           \
+    __builtin_amdgcn_wave_barrier();                                                                 \
   }
+  if constexpr (KG == 1) {
+    PTO_STORE_ROWS(0)
+  } else {
+    if (kg == 0) {
+      PTO_STORE_ROWS(0)
+    } else {
+      PTO_STORE_ROWS(FM / 2)
+    }
+  }
+#undef PTO_STORE_ROWS
   epi.finish(b);
 }
 
