@@ -726,31 +726,30 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
     constexpr int HF = FM / 2, PER = HF * FN;
     static_assert(sizeof(cvec_t) == 16 && NW <= 2 * NS && 2 * PER * 1024 <= Plan::ARR,
                   "K-group exchange: 4-byte accumulators, two waves per stage array");
-    auto slot = [&](int w) -> char* {
-      const int a = w / 2;
-      char* base = a == 0 ? st0 : a == 1 ? st1 : a == 2 ? st2 : st3;
-      return base + (w & 1) * (PER * 1024);
-    };
-    auto exchange = [&](auto send_c, auto keep_c) {
-      constexpr int SEND = decltype(send_c)::value, KEEP = decltype(keep_c)::value;
-      char* mine = slot(wave);
-#pragma unroll
-      for (int e = 0; e < PER; ++e)
-        *reinterpret_cast<cvec_t*>(mine + (e * 64 + lane) * 16) = acc[SEND + e / FN][e % FN];
-      stage_barrier();
-      const char* theirs = slot(kg ? wave - NWG : wave + NWG);
-#pragma unroll
-      for (int e = 0; e < PER; ++e) {
-        const cvec_t o = *reinterpret_cast<const cvec_t*>(theirs + (e * 64 + lane) * 16);
-#pragma unroll
-        for (int r = 0; r < MF::NACC; ++r) acc[KEEP + e / FN][e % FN][r] += o[r];
-      }
-      stage_barrier();  // the arrays host the epilogue staging next
-    };
+    // wave w's block: half of stage array w / 2
+#define PTO_SLOT(w) \
+  (((w) / 2 == 0 ? st0 : (w) / 2 == 1 ? st1 : (w) / 2 == 2 ? st2 : st3) + ((w) & 1) * (PER * 1024))
+#define PTO_EXCHANGE(SEND, KEEP)                                                  \
+  {                                                                               \
+    char* mine = PTO_SLOT(wave);                                                  \
+    _Pragma("unroll") for (int e = 0; e < PER; ++e)                               \
+        *reinterpret_cast<cvec_t*>(mine + (e * 64 + lane) * 16) =                 \
+            acc[(SEND) + e / FN][e % FN];                                         \
+    stage_barrier();                                                              \
+    const char* theirs = PTO_SLOT(kg ? wave - NWG : wave + NWG);                  \
+    _Pragma("unroll") for (int e = 0; e < PER; ++e) {                             \
+      const cvec_t o = *reinterpret_cast<const cvec_t*>(theirs + (e * 64 + lane) * 16); \
+      _Pragma("unroll") for (int r = 0; r < MF::NACC; ++r)                        \
+          acc[(KEEP) + e / FN][e % FN][r] += o[r];                                \
+    }                                                                             \
+    stage_barrier(); /* the arrays host the epilogue staging next */             \
+  }
     if (kg == 0)
-      exchange(std::integral_constant<int, HF>{}, std::integral_constant<int, 0>{});
+      PTO_EXCHANGE(HF, 0)
     else
-      exchange(std::integral_constant<int, 0>{}, std::integral_constant<int, HF>{});
+      PTO_EXCHANGE(0, HF)
+#undef PTO_EXCHANGE
+#undef PTO_SLOT
   }
   // The epilogue for the fragment rows EFM .. EFM + WTE/16 - 1 of this
   // wave's sub-tile (all of them, or with K groups its half), written
