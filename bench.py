@@ -442,7 +442,9 @@ def kernel_probe(torch, ops, hip, dev, which):
     roots    the config-4 fp32 coupled-Newton roots at n = 1024, 2048, 4096
              (100 iterations each), twice;
     ns5      the headline step (32 x 4096² + 32 x 4096x11008 bf16) x3 and one
-             4096² matrix x10."""
+             4096² matrix x10;
+    ns5-single  one 4096² bf16 matrix back to back for 15 s (board power
+             and clock sampled beside it)."""
     if which == "factors":
         g = torch.Generator(device=dev).manual_seed(2)
         G = 1e-2 * torch.randn(4096, 4096, generator=g, device=dev)
@@ -469,6 +471,13 @@ def kernel_probe(torch, ops, hip, dev, which):
         single = inputs[0][:1].contiguous()
         for _ in range(10):
             ops.newton_schulz_orthogonalize(single)
+    elif which == "ns5-single":
+        single = make_ns5_inputs(torch, 1, 4096, 4096, SHAPES[0][3], dev)
+        t_end = time.perf_counter() + 15.0
+        while time.perf_counter() < t_end:
+            for _ in range(100):
+                ops.newton_schulz_orthogonalize(single)
+            torch.cuda.synchronize()
     else:
         raise SystemExit(f"unknown probe {which!r}")
     torch.cuda.synchronize()
@@ -535,8 +544,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="headline only (no factors/roots/optimizer)")
     ap.add_argument("--opt-steps", type=int, default=40)
     ap.add_argument("--traffic-probe", action="store_true", help="one NS5 step + 1 GiB copy, for PMC runs")
-    ap.add_argument("--probe", choices=("factors", "roots", "ns5"), help="a bounded run of one kernel family "
-                    "for rocprofv3, no timing")
+    ap.add_argument("--probe", choices=("factors", "roots", "ns5", "ns5-single"),
+                    help="a bounded run of one kernel family for rocprofv3 or a power sampler, no timing")
     ap.add_argument("--digest-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the ns5_update HBM traffic summary from two PMC runs")
     args = ap.parse_args()
