@@ -120,17 +120,32 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   const int* guard;  // if non-null and guard[b * guard_stride] != 0, matrix b is skipped
   int guard_stride;  // ints between the guard words of consecutive matrices (0: one word)
+  int cus;           // compute units of the device (set by the launcher)
 };
 
-// Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each
-// XCD has its own L2. Renumber so that XCD x runs one contiguous range of
-// logical tiles: the ~32 tiles co-resident on an XCD are then neighbours in
-// the (batch, tile) order and share operand panels in that XCD's L2.
+// Workgroups are dispatched to the 8 XCDs round-robin by linear id, each
+// XCD has its own L2, and all XCDs share the memory-side Infinity Cache.
+// With one tile per CU in flight, workgroups w = k·C .. k·C + C - 1 (C the
+// CU count) run together as round k; they take logical tiles k·C .. k·C +
+// C - 1, XCD x the contiguous block k·C + x·C/8 .. + C/8 - 1. The tiles
+// co-resident on an XCD are then neighbours in the (batch, tile) order and
+// share operand panels in its L2, and the eight XCDs work on the same
+// matrix at once, so each one's panel misses are mostly served by the
+// Infinity Cache rather than HBM (a contiguous 1/8 of all tiles per XCD put
+// eight matrices in flight, 512 MB of NS5 operands against a 256 MB cache:
+// batched NS5 +2%). A last partial round, and launches of fewer than C
+// tiles, give each XCD one contiguous range of what is left.
 constexpr int kXcds = 8;
-__device__ __forceinline__ int xcd_remap(int w, int total) {
+__device__ __forceinline__ int xcd_range(int w, int total) {
   const int q = total / kXcds, r = total % kXcds;
   const int xcd = w % kXcds, slot = w / kXcds;
   return (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+}
+__device__ __forceinline__ int xcd_remap(int w, int total, int cus) {
+  if (cus <= 0 || cus % kXcds != 0) return xcd_range(w, total);
+  const int full = total / cus * cus, per = cus / kXcds;
+  if (w < full) return w / cus * cus + (w % kXcds) * per + (w / kXcds) % per;
+  return full + xcd_range(w - full, total - full);
 }
 
 // Map the linear tile id to (tile_row, tile_col).
@@ -317,7 +332,7 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const int kg = KG == 1 ? 0 : wave / NWG, wl = wave - kg * NWG;  // K group, wave in the group
   const int wm = wl / Cfg::WN, wn = wl % Cfg::WN;
   const int ntile = gridDim.x;  // tiles per matrix
-  const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y);
+  const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y, g.cus);
   const int b = logical / ntile;
   if (g.guard != nullptr && g.guard[(int64_t)b * g.guard_stride] != 0) return;
   int ti, tj;
@@ -938,6 +953,7 @@ template <typename T, class Cfg, bool UPPER, class Epi, bool QN = false, bool PT
 int launch_gemm_cfg(GemmArgs g, const Epi& epi, int batch, hipStream_t stream, const char* name) {
   g.tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
   g.tiles_n = (g.N + Cfg::BN - 1) / Cfg::BN;
+  g.cus = device_cus();
   int64_t tiles = UPPER ? (int64_t)g.tiles_m * (g.tiles_m + 1) / 2 : (int64_t)g.tiles_m * g.tiles_n;
   if (tiles == 0 || batch == 0) return 0;
   // the kernel numbers workgroups across the batch in 32-bit arithmetic
