@@ -338,6 +338,12 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   int ti, tj;
   decode_tile<UPPER>(logical - b * ntile, g.tiles_m, g.tiles_n, ti, tj);
   const int row0 = ti * BM, col0 = tj * BN;
+  // On a diagonal tile of a symmetric product a wave whose sub-tile lies
+  // entirely below the diagonal stores nothing (both epilogue passes use
+  // positions i <= j only). In the two-group schedules it still issues its
+  // share of the DMA and every barrier, but skips its fragment reads and
+  // MFMAs, which saves their energy (the board runs at its power limit).
+  const bool idle = UPPER && (Cfg::PP || KG == 2) && ti == tj && wm * WTM >= (wn + 1) * WTN;
 
   // Per-thread DMA sources: instruction q of this wave fills the 1 KiB of
   // the stage at R0*64 bytes, R0 = 16*(wave*IPW + q) (P rows first, then
@@ -551,11 +557,11 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   stage_barrier();                                            \
   __builtin_amdgcn_sched_barrier(0);
 #define PTO_KG_R(J, RD, DMA)                                  \
-  load_frags(RD, f);                                          \
+  if (!idle) load_frags(RD, f);                               \
   issue(min((J) + 3, KT - 1), DMA);                           \
   PTO_KG_END()
 #define PTO_KG_M(J, DMA)                                      \
-  mma(f);                                                     \
+  if (!idle) mma(f);                                          \
   issue(min((J) + 3, KT - 1), DMA);                           \
   PTO_KG_END()
       if (kg == 0) {
@@ -613,13 +619,13 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
       }
       for (int kt = 0; kt < KT; kt += kStages) {
 #define PTO_PP(J, RD, DMA)                                    \
-  load_frags(RD, f);                                          \
+  if (!idle) load_frags(RD, f);                               \
   issue(min(kt + (J) + 3, KT - 1), DMA);                      \
   __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));             \
   __builtin_amdgcn_sched_barrier(0);                          \
   stage_barrier();                                            \
   __builtin_amdgcn_sched_barrier(0);                          \
-  mma(f);                                                     \
+  if (!idle) mma(f);                                          \
   __builtin_amdgcn_s_waitcnt(PTO_VMCNT(2 * IPW));             \
   __builtin_amdgcn_sched_barrier(0);                          \
   stage_barrier();                                            \
