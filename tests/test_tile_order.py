@@ -14,6 +14,9 @@ fewer than C tiles) one contiguous range per XCD. Checked here:
 
 Planted mistakes (the XCD and slot roles swapped, a wrong slot modulus, the
 tail without its offset) fail one of these.
+
+The blocked order of upper (symmetric-product) tiles used for bf16 (blocks
+of 4 tile rows x 8 tile columns) must enumerate exactly the tiles i <= j.
 """
 
 import pytest
@@ -71,3 +74,42 @@ def test_tile_order_planted_mistakes_are_caught(plant):
     with pytest.raises(AssertionError):
         for total in (256, 8704, 22016 + 37):
             _check(total, 256, plant)
+
+
+def _decode_blocked(t, n, br=4, bc=8):
+    """decode_tile<UPPER, BLOCKED> of the kernel."""
+    rem = t
+    for r0 in range(0, n, br):
+        r1 = min(r0 + br, n)
+        for c0 in range((r0 // bc) * bc, n, bc):
+            c1 = min(c0 + bc, n)
+            cnt = sum(max(0, c1 - max(c0, i)) for i in range(r0, r1))
+            if rem < cnt:
+                for i in range(r0, r1):
+                    k = max(0, c1 - max(c0, i))
+                    if rem < k:
+                        return i, max(c0, i) + rem
+                    rem -= k
+            rem -= cnt
+    return None
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 8, 9, 16, 17, 22, 33, 43])
+def test_blocked_upper_order_enumerates_upper_tiles(n):
+    got = [_decode_blocked(t, n) for t in range(n * (n + 1) // 2)]
+    assert None not in got and len(set(got)) == len(got)
+    assert all(0 <= i <= j < n for i, j in got)
+
+
+def test_blocked_upper_order_reads_fewer_panels():
+    # a 22 x 22 grid (4096 / 192, the K-FAC Gram): runs of 32 consecutive tiles
+    # (what one XCD runs at once) touch 14-18 distinct operand panels against
+    # 16-22 for whole upper-triangle rows
+    n = 22
+
+    def panels(seq):
+        return [len({i for i, _ in seq[s:s + 32]} | {j for _, j in seq[s:s + 32]}) for s in range(0, len(seq), 32)]
+
+    blocked = panels([_decode_blocked(t, n) for t in range(n * (n + 1) // 2)])
+    plain = panels([(i, j) for i in range(n) for j in range(i, n)])
+    assert max(blocked) < max(plain) and sum(blocked) < sum(plain)
