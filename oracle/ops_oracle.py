@@ -1,7 +1,8 @@
 """CPU oracle for the pytorch_opt.ops hot path — TEST INFRASTRUCTURE ONLY.
 
-Plain numpy restatement of the reference algorithms, used as the checker by
-tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg. Nothing in
+Plain numpy restatement of the reference algorithms, against which
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg check the
+HIP kernels. Nothing in
 the product imports this module.
 
 Every function cites the reference lines it restates (paths relative to

@@ -33,7 +33,7 @@ def _seed():
 
 @pytest.fixture(scope="session")
 def hip():
-    """The loaded HIP backend. On a GPU box a missing library is a failure,
+    """The loaded HIP backend. With a GPU present a missing library is a failure,
     never a silent fallback."""
     from pytorch_opt import ops
 

@@ -1,5 +1,5 @@
 """KronTracker (factor statistics through ops.gram_update_) against brute
-force, on CPU and, on a GPU box, through the HIP Gram kernel:
+force, on CPU and, with a GPU, through the HIP Gram kernel:
 
 * A and G of a Linear layer equal sums of per-row outer products;
 * the blend schedule over three batches (EMA weights β², β(1−β), 1−β; the

@@ -1,4 +1,4 @@
-"""SOAP against closed forms, on CPU and, on a GPU box, through the HIP
+"""SOAP against closed forms, on CPU and, with a GPU, through the HIP
 kernels (factor updates, eigenbasis rotations, second-moment transport):
 
 * gradients supported on one permutation pattern keep both factors
