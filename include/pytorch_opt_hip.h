@@ -85,6 +85,19 @@ int pto_kron_factor_update(void* L, void* R, const void* G, int dtype, int64_t m
                            void* workspace, size_t ws_bytes, void* stream);
 
 /*
+ * Batched factor update (additive; the reference updates one parameter's
+ * factors per call, pytorch_opt/optim/shampoo.py:98-100 and
+ * pytorch_opt/optim/soap.py:88-90): for b < batch,
+ *   L[b] <- beta2*L[b] + (1-beta2)*G[b]*G[b]^T,  R[b] <- ... G[b]^T*G[b].
+ * G is one contiguous stack [batch][m][n]; L and R are host arrays of
+ * batch device pointers to distinct [m,m] / [n,n] tensors. batch <= 64.
+ * Each factor gets exactly the bits pto_kron_factor_update gives it.
+ */
+size_t pto_kron_batched_workspace_bytes(int dtype, int64_t batch, int64_t m, int64_t n);
+int pto_kron_factor_update_batched(void* const* L, void* const* R, const void* G, int dtype, int64_t batch, int64_t m,
+                                   int64_t n, double beta2, void* workspace, size_t ws_bytes, void* stream);
+
+/*
  * Gram update F <- beta*F + alpha * Xa^T Xa, Xa = [X, 1] if append_ones.
  * The reference has no compiled counterpart: it is the boundary added for
  * the K-FAC factor products pytorch_opt/curvature/kron.py:105-113 and the

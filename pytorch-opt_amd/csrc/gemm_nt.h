@@ -1316,4 +1316,34 @@ struct EpiBlend {
   __device__ __forceinline__ void finish(int) const {}
 };
 
+// EpiBlend over up to kBlendTab separately allocated outputs of one shape:
+// matrix b of the launch blends into dst[b] (row pitch ld). The table
+// travels in the kernel arguments, so it needs no device copy.
+constexpr int kBlendTab = 64;
+template <typename TO, typename A>
+struct EpiBlendTab {
+  typedef A S;
+  TO* dst[kBlendTab];
+  int64_t ld;
+  A beta, alpha;
+  bool vec;
+  typedef Raw8<TO> Pre;
+  typedef Raw8<TO> PreT;
+  static constexpr bool kVoIsV = true;
+  __device__ __forceinline__ EpiBlend<TO, A> one(int b) const { return EpiBlend<TO, A>{dst[b], ld, 0, beta, alpha, vec}; }
+  __device__ __forceinline__ bool has_t() const { return false; }
+  __device__ __forceinline__ void load(int b, int i, int j0, int kbeg, int n, Pre& p) const {
+    one(b).load(0, i, j0, kbeg, n, p);
+  }
+  __device__ __forceinline__ void load_t(int b, int j, int i0, int n, PreT& p) const { one(b).load_t(0, j, i0, n, p); }
+  __device__ __forceinline__ void put(int b, int i, int j0, const S* v, int kbeg, int n, const Pre& pre,
+                                      S* vo) const {
+    one(b).put(0, i, j0, v, kbeg, n, pre, vo);
+  }
+  __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT& pre) const {
+    one(b).put_t(0, j, i0, v, n, pre);
+  }
+  __device__ __forceinline__ void finish(int) const {}
+};
+
 }  // namespace pto

@@ -67,6 +67,73 @@ int kron_t(T* L, T* R, const T* G, int64_t m, int64_t n, double beta2, void* ws,
   return 0;
 }
 
+// Batched form for the optimizers, which update many same-shape factors per
+// step: G is one stacked tensor [batch][m][n] (the caller stacks the
+// gradients), L[b] and R[b] are separate tensors reached through a pointer
+// table. Each side is one launch over the whole batch; every fp32/fp64 tile
+// sums a position's products in the same order, so each factor gets exactly
+// the bits a single-matrix call gives.
+template <typename T>
+size_t kron_batched_ws_bytes_t(int64_t batch, int64_t m, int64_t n) {
+  int64_t ldm = round_up(m, kPadK), ldn = round_up(n, kPadK);
+  size_t bytes = 0;
+  auto add = [&](size_t b) { bytes = round_up(bytes, 256) + b; };
+  add(sizeof(T) * batch * m * ldn);  // G padded (only when n is not a pad multiple)
+  add(sizeof(T) * batch * n * ldm);  // Gᵀ
+  return bytes + 256;
+}
+
+template <typename T>
+int kron_batched_t(T* const* L, T* const* R, const T* G, int64_t batch, int64_t m, int64_t n, double beta2, void* ws,
+                   size_t ws_bytes, hipStream_t stream) {
+  typedef typename AccOf<T>::type A;
+  PTO_REQUIRE(m <= INT32_MAX && n <= INT32_MAX, "kron_factor_update_batched_: shape too large");
+  PTO_REQUIRE(batch >= 0 && batch <= kBlendTab, "kron_factor_update_batched_: at most 64 matrices per call");
+  if (batch == 0 || m == 0 || n == 0) return 0;
+  for (int64_t b = 0; b < batch; ++b) {
+    PTO_REQUIRE(L[b] && R[b], "kron_factor_update_batched_: null factor");
+    for (int64_t c = 0; c < batch; ++c)
+      PTO_REQUIRE(L[b] != R[c] && (c == b || (L[b] != L[c] && R[b] != R[c])),
+                  "kron_factor_update_batched_: factors must be distinct tensors");
+  }
+  const int64_t ldm = round_up(m, kPadK), ldn = round_up(n, kPadK);
+  Carver cv(ws, ws_bytes);
+  T* Gp = cv.take<T>(batch * m * ldn);
+  T* GT = cv.take<T>(batch * n * ldm);
+  PTO_REQUIRE(!cv.overflow, "kron_factor_update_batched_: workspace too small");
+
+  const bool direct = (n % kPadK == 0) && (reinterpret_cast<uintptr_t>(G) & 15) == 0;
+  const T* Grows = direct ? G : Gp;
+  const int64_t ldg = direct ? n : ldn, sg = direct ? m * n : m * ldn;
+  if (launch_pack<T, T, A>(G, m, n, n, m * n, nullptr, direct ? nullptr : Gp, ldn, m * ldn, GT, ldm, n * ldm, false,
+                           (int)batch, stream))
+    return -1;
+
+  const A beta = beta2 == 1.0 ? A(1) : static_cast<A>(beta2);
+  const A alpha = beta2 == 1.0 ? A(1) : static_cast<A>(1.0 - beta2);
+  auto table = [&](T* const* F, int64_t d) {
+    EpiBlendTab<T, A> e{};
+    e.ld = d;
+    e.beta = beta;
+    e.alpha = alpha;
+    e.vec = true;
+    for (int64_t b = 0; b < batch; ++b) {
+      e.dst[b] = F[b];
+      e.vec = e.vec && vec_ok<T>(F[b], d, 0);
+    }
+    return e;
+  };
+  {
+    GemmArgs g{Grows, ldg, sg, Grows, ldg, sg, (int)m, (int)m, (int)ldn, 0, 0, nullptr};
+    if (launch_gemm<T, true>(g, table(L, m), (int)batch, stream, "kron_left")) return -1;
+  }
+  {
+    GemmArgs g{GT, ldm, n * ldm, GT, ldm, n * ldm, (int)n, (int)n, (int)ldm, 0, 0, nullptr};
+    if (launch_gemm<T, true>(g, table(R, n), (int)batch, stream, "kron_right")) return -1;
+  }
+  return 0;
+}
+
 // bf16 X without the ones column is already the [K][M] operand of the
 // transposing-read layout (K = tokens, M = features), for both sides of
 // X̃ᵀX̃: it is read in place, with no Xᵀ pass and no workspace, when the
@@ -151,6 +218,37 @@ int pto_kron_factor_update(void* L, void* R, const void* G, int dtype, int64_t m
                                  n, beta2, workspace, ws_bytes, s);
     default:
       PTO_REQUIRE(false, "kron_factor_update_: unsupported dtype code");
+  }
+}
+
+size_t pto_kron_batched_workspace_bytes(int dtype, int64_t batch, int64_t m, int64_t n) {
+  switch (dtype) {
+    case pto::kBF16: return pto::kron_batched_ws_bytes_t<pto::bf16>(batch, m, n);
+    case pto::kF32: return pto::kron_batched_ws_bytes_t<float>(batch, m, n);
+    case pto::kF64: return pto::kron_batched_ws_bytes_t<double>(batch, m, n);
+    default: return 0;
+  }
+}
+
+int pto_kron_factor_update_batched(void* const* L, void* const* R, const void* G, int dtype, int64_t batch, int64_t m,
+                                   int64_t n, double beta2, void* workspace, size_t ws_bytes, void* stream) {
+  PTO_REQUIRE(batch >= 0 && m >= 0 && n >= 0, "kron_factor_update_batched_: negative extent");
+  PTO_REQUIRE(batch * m * n == 0 || (L && R && G && workspace),
+              "kron_factor_update_batched_: null factor table, gradient stack or workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case pto::kBF16:
+      return pto::kron_batched_t<pto::bf16>(reinterpret_cast<pto::bf16* const*>(L),
+                                            reinterpret_cast<pto::bf16* const*>(R),
+                                            static_cast<const pto::bf16*>(G), batch, m, n, beta2, workspace, ws_bytes, s);
+    case pto::kF32:
+      return pto::kron_batched_t<float>(reinterpret_cast<float* const*>(L), reinterpret_cast<float* const*>(R),
+                                        static_cast<const float*>(G), batch, m, n, beta2, workspace, ws_bytes, s);
+    case pto::kF64:
+      return pto::kron_batched_t<double>(reinterpret_cast<double* const*>(L), reinterpret_cast<double* const*>(R),
+                                         static_cast<const double*>(G), batch, m, n, beta2, workspace, ws_bytes, s);
+    default:
+      PTO_REQUIRE(false, "kron_factor_update_batched_: unsupported dtype code");
   }
 }
 

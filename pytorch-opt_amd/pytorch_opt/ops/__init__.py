@@ -108,6 +108,18 @@ def kron_factor_update_(L, R, G, beta2=1.0):
     return reference.kron_factor_update_(L, R, G, beta2=beta2)
 
 
+def kron_factor_update_batched_(Ls, Rs, Gs, beta2=1.0):
+    """kron_factor_update_ of each (L, R, G) in three same-length lists of
+    same-shape tensors (additive: the optimizers' per-step factor updates as
+    one call); each pair gets what a separate kron_factor_update_ gives it."""
+    if _use_native():
+        _NATIVE.kron_factor_update_batched_(list(Ls), list(Rs), list(Gs), float(beta2))
+        return Ls, Rs
+    for L, R, G in zip(Ls, Rs, Gs):
+        reference.kron_factor_update_(L, R, G, beta2=beta2)
+    return Ls, Rs
+
+
 def precond_apply_two_sided(L_root, G, R_root):
     if _use_native():
         return _NATIVE.precond_apply_two_sided(L_root, G, R_root)
@@ -142,7 +154,8 @@ def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
 
 __all__ = ["get_backend", "set_backend", "native_available", "load_native", "inverse_matrix_root",
            "inverse_matrix_root_each",
-           "newton_schulz_orthogonalize", "kron_factor_update_", "precond_apply_two_sided",
+           "newton_schulz_orthogonalize", "kron_factor_update_", "kron_factor_update_batched_",
+           "precond_apply_two_sided",
            "two_sided_product", "gram_update_", "adamw_step_", "OpsArgumentError", "reference"]
 
 if os.environ.get("PYTORCH_OPT_NATIVE") == "1":

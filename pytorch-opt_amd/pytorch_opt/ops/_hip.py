@@ -63,6 +63,9 @@ SIGNATURES = {
     "pto_two_sided_product_batched_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "pto_two_sided_product_batched": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_i64, _c_i64,
                                                _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_ptr, _c_size, _c_ptr]),
+    "pto_kron_batched_workspace_bytes": (_c_size, [_c_int, _c_i64, _c_i64, _c_i64]),
+    "pto_kron_factor_update_batched": (_c_int, [ctypes.POINTER(_c_ptr), ctypes.POINTER(_c_ptr), _c_ptr, _c_int, _c_i64,
+                                                _c_i64, _c_i64, _c_dbl, _c_ptr, _c_size, _c_ptr]),
     "pto_adamw_workspace_bytes": (_c_size, []),
     "pto_adamw_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_dbl, _c_dbl, _c_dbl,
                                 _c_dbl, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
@@ -181,6 +184,42 @@ class HipBackend:
             L.copy_(Lw)
         if Rw is not R:
             R.copy_(Rw)
+
+    # matrices per launch of the batched factor update (its epilogue's table)
+    KRON_BATCH = 64
+
+    def kron_factor_update_batched_(self, Ls, Rs, Gs, beta2):
+        """kron_factor_update_ on each (L, R, G) of same-shape lists, one launch
+        per side for up to KRON_BATCH matrices; each factor gets the bits the
+        single call gives it. The gradients are stacked into one tensor."""
+        k = len(Gs)
+        if not (len(Ls) == len(Rs) == k):
+            raise OpsArgumentError("kron_factor_update_batched_: L, R and G lists differ in length")
+        if k == 0:
+            return
+        m, n = Gs[0].shape if Gs[0].dim() == 2 else (None, None)
+        if m is None or any(G.dim() != 2 or tuple(G.shape) != (m, n) for G in Gs):
+            raise OpsArgumentError("kron_factor_update_batched_: every G must be 2D with one shape")
+        dev, dt = Ls[0].device, Ls[0].dtype
+        same = all(t.device == dev and t.dtype == dt and t.is_contiguous() for t in list(Ls) + list(Rs))
+        if (not same or dt not in _DTYPE_CODE or not dev.type == "cuda"
+                or any(tuple(L.shape) != (m, m) for L in Ls) or any(tuple(R.shape) != (n, n) for R in Rs)):
+            for L, R, G in zip(Ls, Rs, Gs):  # mixed layouts: one call each
+                self.kron_factor_update_(L, R, G, beta2)
+            return
+        code = _DTYPE_CODE[dt]
+        for c0 in range(0, k, self.KRON_BATCH):
+            cl, cr = Ls[c0:c0 + self.KRON_BATCH], Rs[c0:c0 + self.KRON_BATCH]
+            Gst = torch.stack([G.to(device=dev, dtype=dt) for G in Gs[c0:c0 + self.KRON_BATCH]])
+            b = len(cl)
+            lt = (_c_ptr * b)(*[t.data_ptr() for t in cl])
+            rt = (_c_ptr * b)(*[t.data_ptr() for t in cr])
+            with torch.cuda.device(dev):
+                nbytes = self._lib.pto_kron_batched_workspace_bytes(code, b, m, n)
+                ws = self._workspace(nbytes, dev)
+                rc = self._lib.pto_kron_factor_update_batched(lt, rt, _ptr(Gst), code, b, m, n, float(beta2),
+                                                              _ptr(ws), nbytes, self._stream(dev))
+            self._check(rc, "kron_factor_update_batched_")
 
     @staticmethod
     def newton_for(method: str) -> bool:

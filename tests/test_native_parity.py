@@ -213,6 +213,64 @@ def test_kron_nonsymmetric_prior_and_fp64(native_backend, m, n):
     assert np.abs(_np(L) - Lo).max() < 1e-12 and np.abs(_np(R) - Ro).max() < 1e-12
 
 
+@pytest.mark.parametrize("dtype,k,m,n,beta2", [
+    (torch.float32, 5, 200, 300, 0.95),     # ragged: G padded, small tiles
+    (torch.float32, 48, 2048, 2048, 0.999),  # Shampoo's config-5 attention factors
+    (torch.float32, 70, 96, 64, 1.0),       # two launches (64 per call), plain sums
+    (torch.float64, 6, 130, 257, 0.9),
+])
+def test_kron_batched_matches_single_calls(native_backend, hip, dtype, k, m, n, beta2):
+    """One kron_factor_update_batched_ call gives every factor exactly the
+    bits of its own kron_factor_update_ call (fp32/fp64 tiles all sum a
+    position's products in one order), and it launched batched kernels."""
+    g = torch.Generator(device=DEV).manual_seed(k * 1000 + m)
+    Gs = [1e-2 * torch.randn(m, n, generator=g, device=DEV, dtype=dtype) for _ in range(k)]
+    Ls = [torch.randn(m, m, generator=g, device=DEV, dtype=dtype) for _ in range(k)]
+    Rs = [torch.randn(n, n, generator=g, device=DEV, dtype=dtype) for _ in range(k)]
+    L1, R1 = [L.clone() for L in Ls], [R.clone() for R in Rs]
+    for L, R, G in zip(L1, R1, Gs):
+        ops.kron_factor_update_(L, R, G, beta2=beta2)
+    torch.cuda.synchronize()
+    hip.prof_reset()
+    hip.prof_enable(True)
+    ops.kron_factor_update_batched_(Ls, Rs, Gs, beta2=beta2)
+    torch.cuda.synchronize()
+    hip.prof_enable(False)
+    assert hip.prof_query("kron_left")[1] == (k + 63) // 64
+    for i in range(k):
+        assert torch.equal(Ls[i], L1[i]) and torch.equal(Rs[i], R1[i]), i
+
+
+def test_kron_batched_bf16_and_fallbacks(native_backend):
+    """bf16 factors (the batched launch may pick another tile and sum in
+    another order: vs float64 at bf16 accuracy), mixed layouts (one call
+    each) and argument errors."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    Gs = [torch.randn(300, 200, generator=g, device=DEV).bfloat16() for _ in range(3)]
+    Ls = [torch.zeros(300, 300, device=DEV).bfloat16() for _ in range(3)]
+    Rs = [torch.zeros(200, 200, device=DEV).bfloat16() for _ in range(3)]
+    ops.kron_factor_update_batched_(Ls, Rs, Gs, beta2=1.0)
+    for L, R, G in zip(Ls, Rs, Gs):
+        Gd = G.double()
+        assert float((L.double() - Gd @ Gd.T).norm() / (Gd @ Gd.T).norm()) < 1e-2
+        assert float((R.double() - Gd.T @ Gd).norm() / (Gd.T @ Gd).norm()) < 1e-2
+    # a non-contiguous factor takes the per-matrix path, with the same result
+    G = torch.randn(64, 48, generator=g, device=DEV)
+    Lt = torch.randn(64, 64, generator=g, device=DEV).T
+    R0 = torch.randn(48, 48, generator=g, device=DEV)
+    L1, R1 = Lt.clone(), R0.clone()
+    ops.kron_factor_update_(L1, R1, G, beta2=0.9)
+    L2, R2 = Lt.clone().T.contiguous().T, R0.clone()
+    ops.kron_factor_update_batched_([L2], [R2], [G], beta2=0.9)
+    assert torch.equal(L1, L2) and torch.equal(R1, R2)
+    with pytest.raises(ValueError):
+        ops.kron_factor_update_batched_([L2], [R2, R2], [G], beta2=0.9)
+    with pytest.raises(RuntimeError):
+        same = torch.zeros(64, 64, device=DEV)
+        ops.kron_factor_update_batched_([same, same], [torch.zeros(48, 48, device=DEV)] * 2,
+                                        [G, G], beta2=0.9)
+
+
 def test_kron_config3_full_size(native_backend):
     """fp32 G 4096² ~ N(0,1e-2), β=0.95, priors = Gram matrices of G0."""
     g = torch.Generator(device=DEV).manual_seed(2)
