@@ -185,13 +185,18 @@ class HipBackend:
         if Rw is not R:
             R.copy_(Rw)
 
-    # matrices per launch of the batched factor update (its epilogue's table)
+    # matrices per launch of the batched factor update (its epilogue's
+    # table), and the bytes of stacked gradients per launch: the stack and
+    # the workspace (Gᵀ and, for unpadded widths, a padded G) are transient
+    # copies of about that size each
     KRON_BATCH = 64
+    KRON_BATCH_BYTES = 1 << 30
 
     def kron_factor_update_batched_(self, Ls, Rs, Gs, beta2):
         """kron_factor_update_ on each (L, R, G) of same-shape lists, one launch
-        per side for up to KRON_BATCH matrices; each factor gets the bits the
-        single call gives it. The gradients are stacked into one tensor."""
+        per side for up to KRON_BATCH matrices and KRON_BATCH_BYTES of
+        gradients; each factor gets the bits the single call gives it. The
+        gradients of a launch are stacked into one tensor."""
         k = len(Gs)
         if not (len(Ls) == len(Rs) == k):
             raise OpsArgumentError("kron_factor_update_batched_: L, R and G lists differ in length")
@@ -208,9 +213,11 @@ class HipBackend:
                 self.kron_factor_update_(L, R, G, beta2)
             return
         code = _DTYPE_CODE[dt]
-        for c0 in range(0, k, self.KRON_BATCH):
-            cl, cr = Ls[c0:c0 + self.KRON_BATCH], Rs[c0:c0 + self.KRON_BATCH]
-            Gst = torch.stack([G.to(device=dev, dtype=dt) for G in Gs[c0:c0 + self.KRON_BATCH]])
+        g_bytes = max(m * n * (torch.finfo(dt).bits // 8), 1)
+        per = max(1, min(self.KRON_BATCH, self.KRON_BATCH_BYTES // g_bytes))
+        for c0 in range(0, k, per):
+            cl, cr = Ls[c0:c0 + per], Rs[c0:c0 + per]
+            Gst = torch.stack([G.to(device=dev, dtype=dt) for G in Gs[c0:c0 + per]])
             b = len(cl)
             lt = (_c_ptr * b)(*[t.data_ptr() for t in cl])
             rt = (_c_ptr * b)(*[t.data_ptr() for t in cr])

@@ -241,6 +241,29 @@ def test_kron_batched_matches_single_calls(native_backend, hip, dtype, k, m, n, 
         assert torch.equal(Ls[i], L1[i]) and torch.equal(Rs[i], R1[i]), i
 
 
+def test_kron_batched_byte_cap(native_backend, hip, monkeypatch):
+    """A launch stacks at most KRON_BATCH_BYTES of gradients: seven 64x96
+    fp32 gradients under a cap of three run as three launches per side,
+    each factor still with the bits of its own single call."""
+    monkeypatch.setattr(hip, "KRON_BATCH_BYTES", 3 * 64 * 96 * 4)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    Gs = [torch.randn(64, 96, generator=g, device=DEV) for _ in range(7)]
+    Ls = [torch.randn(64, 64, generator=g, device=DEV) for _ in range(7)]
+    Rs = [torch.randn(96, 96, generator=g, device=DEV) for _ in range(7)]
+    L1, R1 = [L.clone() for L in Ls], [R.clone() for R in Rs]
+    for L, R, G in zip(L1, R1, Gs):
+        ops.kron_factor_update_(L, R, G, beta2=0.95)
+    torch.cuda.synchronize()
+    hip.prof_reset()
+    hip.prof_enable(True)
+    ops.kron_factor_update_batched_(Ls, Rs, Gs, beta2=0.95)
+    torch.cuda.synchronize()
+    hip.prof_enable(False)
+    assert hip.prof_query("kron_left")[1] == 3 and hip.prof_query("kron_right")[1] == 3
+    for i in range(7):
+        assert torch.equal(Ls[i], L1[i]) and torch.equal(Rs[i], R1[i]), i
+
+
 def test_kron_batched_bf16_and_fallbacks(native_backend):
     """bf16 factors (the batched launch may pick another tile and sum in
     another order: vs float64 at bf16 accuracy), mixed layouts (one call
