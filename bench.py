@@ -444,7 +444,12 @@ def kernel_probe(torch, ops, hip, dev, which):
     ns5      the headline step (32 x 4096² + 32 x 4096x11008 bf16) x3 and one
              4096² matrix x10;
     ns5-single  one 4096² bf16 matrix back to back for 15 s (board power
-             and clock sampled beside it)."""
+             and clock sampled beside it);
+    shampoo  the fp32 2048² work of a plain Shampoo step on the 48
+             attention matrices: the batched factor update (48 x (L, R),
+             beta 0.999) x10, the two-sided apply L·G·R as one batched call
+             over the stacked 48 x10, and as 48 single calls (the harness's
+             per-parameter form) x2."""
     if which == "factors":
         g = torch.Generator(device=dev).manual_seed(2)
         G = 1e-2 * torch.randn(4096, 4096, generator=g, device=dev)
@@ -478,6 +483,21 @@ def kernel_probe(torch, ops, hip, dev, which):
             for _ in range(100):
                 ops.newton_schulz_orthogonalize(single)
             torch.cuda.synchronize()
+    elif which == "shampoo":
+        g = torch.Generator(device=dev).manual_seed(6)
+        Gs = [1e-2 * torch.randn(2048, 2048, generator=g, device=dev) for _ in range(48)]
+        Ls = [torch.eye(2048, device=dev) for _ in range(48)]
+        Rs = [torch.eye(2048, device=dev) for _ in range(48)]
+        for _ in range(10):
+            ops.kron_factor_update_batched_(Ls, Rs, Gs, beta2=0.999)
+        Gst = torch.stack(Gs)
+        Lr = torch.stack(Ls) * (1.0 / Ls[0].norm())
+        Rr = torch.stack(Rs) * (1.0 / Rs[0].norm())
+        for _ in range(10):
+            ops.precond_apply_two_sided(Lr, Gst, Rr)
+        for _ in range(2):
+            for i in range(48):
+                ops.precond_apply_two_sided(Lr[i], Gs[i], Rr[i])
     else:
         raise SystemExit(f"unknown probe {which!r}")
     torch.cuda.synchronize()
@@ -544,7 +564,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="headline only (no factors/roots/optimizer)")
     ap.add_argument("--opt-steps", type=int, default=40)
     ap.add_argument("--traffic-probe", action="store_true", help="one NS5 step + 1 GiB copy, for PMC runs")
-    ap.add_argument("--probe", choices=("factors", "roots", "ns5", "ns5-single"),
+    ap.add_argument("--probe", choices=("factors", "roots", "ns5", "ns5-single", "shampoo"),
                     help="a bounded run of one kernel family for rocprofv3 or a power sampler, no timing")
     ap.add_argument("--digest-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the ns5_update HBM traffic summary from two PMC runs")
