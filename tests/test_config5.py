@@ -1,7 +1,8 @@
 """Config 5 at its real shapes and settings: the synthetic 12-layer d=2048
 parameter set and per-step gradients of bench.py (same seeds), the Muon arm
-and the Shampoo arm teacher-forced against the numpy oracle at steps 0, 1
-and 20 (two root refreshes and a stale-root step between them).
+and the Shampoo arm teacher-forced against the numpy oracle at steps 0, 1,
+20 and 39 of the 40-step run (two root refreshes, a stale-root step
+between them and the last step, 19 steps after the second refresh).
 
 A subset of the matrices is optimised (every matrix's update is independent
 of the others'), so the CPU oracle stays within seconds:
@@ -24,8 +25,8 @@ import torch
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-CHECK = (0, 1, 20)
-STEPS = 21
+CHECK = (0, 1, 20, 39)
+STEPS = 40
 
 
 def _params_and_grads():
