@@ -51,6 +51,9 @@ int pto_runtime_version(void);
  * pytorch_opt/ops/reference.py:71-97 and csrc/pytorch_opt_ops.cpp:65-81.
  * G and out are [batch, rows, cols] of `dtype`. bf16 computes with bf16
  * operands and fp32 accumulation; f32/f64 stay in their own precision.
+ * out may be G itself (in place) but must not otherwise overlap it. G may
+ * sit at any element alignment (a G that is not 16-byte aligned is copied
+ * into the workspace first).
  */
 size_t pto_ns5_workspace_bytes(int dtype, int64_t batch, int64_t rows, int64_t cols);
 int pto_ns5(const void* G, void* out, int dtype, int64_t batch, int64_t rows, int64_t cols, int64_t steps,
@@ -91,7 +94,10 @@ int pto_kron_factor_update(void* L, void* R, const void* G, int dtype, int64_t m
  *   L[b] <- beta2*L[b] + (1-beta2)*G[b]*G[b]^T,  R[b] <- ... G[b]^T*G[b].
  * G is one contiguous stack [batch][m][n]; L and R are host arrays of
  * batch device pointers to distinct [m,m] / [n,n] tensors. batch <= 64.
- * Each factor gets exactly the bits pto_kron_factor_update gives it.
+ * In f32 and f64 each factor gets exactly the bits pto_kron_factor_update
+ * gives it. In bf16 the tile the library picks depends on the batch, and
+ * the 192x192 tile sums even and odd K tiles in separate accumulators, so
+ * a batched result may differ from the single call's in the last bits.
  */
 size_t pto_kron_batched_workspace_bytes(int dtype, int64_t batch, int64_t m, int64_t n);
 int pto_kron_factor_update_batched(void* const* L, void* const* R, const void* G, int dtype, int64_t batch, int64_t m,

@@ -745,9 +745,14 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   // disjoint positions, so the early reads see the values from before the
   // launch.
   // In symmetric (UPPER) products the value for (i, j), i <= j, is stored
-  // at (i, j) by its own direct pass and at (j, i) by its transposed pass;
-  // on diagonal tiles positions below the diagonal are skipped by the
-  // direct pass, so the stored matrix is exactly symmetric.
+  // at (i, j) by its own direct pass and at (j, i) by its transposed pass,
+  // so the stored matrix is exactly symmetric. On diagonal tiles the 8x8
+  // blocks on the diagonal are written whole by the direct pass, each
+  // position below the diagonal taking the staged value of its mirror
+  // (j, i), so every run stays a full 16-byte access (partial runs there
+  // made the diagonal tiles' epilogue 1.5-2x longer than the others' and
+  // the last to finish); the transposed pass covers the rest below the
+  // diagonal.
   constexpr int RPP = Plan::RPP, SP = Plan::SP, WTE = Plan::WTE;
   const int wa = wave / Plan::WPA;  // < NS
   char* arr = wa == 0 ? st0 : wa == 1 ? st1 : wa == 2 ? st2 : wa == 3 ? st3 : wa == 4 ? st4 : wa == 5 ? st5 : wa == 6 ? st6 : st7;
@@ -821,7 +826,8 @@ _Pragma("unroll")                                                               
       const int c = ((it % CBLK) * LGD + lane % LGD) * 8;                                            \
       const int i = pr0 + r, j0 = wc0 + c;                                                           \
       const int n = min(8, nrem - c);                                                                \
-      const int kbeg = diag ? max(0, i - j0) : 0;  /* skip i > j on diagonal tiles */                \
+      /* diagonal tiles: skip runs below the diagonal; a run inside an 8x8 block on it is full */     \
+      const int kbeg = diag && i - j0 >= 8 ? 8 : 0;                                                  \
       if (lane_ok && r < rows && c < nrem && kbeg < n) epi.load(b, i, j0, kbeg, n, pre[it]);         \
     }                                                                                                \
 _Pragma("unroll")                                                                                    \
@@ -842,13 +848,22 @@ _Pragma("unroll")                                                               
       const int c = ((it % CBLK) * LGD + lane % LGD) * 8;                                            \
       const int i = pr0 + r, j0 = wc0 + c;                                                           \
       const int n = min(8, nrem - c);                                                                \
-      const int kbeg = diag ? max(0, i - j0) : 0;                                                    \
+      const int kbeg = diag && i - j0 >= 8 ? 8 : 0;                                                  \
       if (!(lane_ok && r < rows && c < nrem && kbeg < n)) continue;                                  \
+      /* dk in 1..7: the run crosses the diagonal; its positions k < dk lie below it and take the  \
+         mirrored value, staged at row j0 + k, column i of the same slab (the 16-aligned slab holds \
+         the whole 8-row group; those diagonal-block entries are never written back) */            \
       S v[8], vo[8];                                                                                 \
 _Pragma("unroll")                                                                                    \
       for (int k = 0; k < 8; ++k) v[k] = stg[r * SP + c + k];                                        \
+      if (diag && i - j0 > 0) {                                                                      \
+        const int dk = i - j0;                                                                       \
+_Pragma("unroll")                                                                                    \
+        for (int k = 0; k < 7; ++k)                                                                  \
+          if (k < dk) v[k] = stg[(c + k - (pr0 - wc0)) * SP + r + (pr0 - wc0)];                      \
+      }                                                                                              \
       epi.put(b, i, j0, v, kbeg, n, pre[it], vo);                                                    \
-      if (need_t && !Epi::kVoIsV) {                                                                  \
+      if (need_t && !Epi::kVoIsV && !(diag && i - j0 >= 0)) {                                        \
 _Pragma("unroll")                                                                                    \
         for (int k = 0; k < 8; ++k) stg[r * SP + c + k] = vo[k];                                     \
       }                                                                                              \
@@ -866,7 +881,7 @@ _Pragma("unroll")                                                               
         const int r = ((it / CBT) * 8 + lane % 8) * 8;                                               \
         const int j = wc0 + c, i0 = pr0 + r;                                                         \
         int n = min(8, rows - r);                                                                    \
-        if (diag) n = min(n, j - i0);  /* strictly below the diagonal */                             \
+        if (diag && j - i0 < 8) n = 0;  /* below the diagonal, outside its 8x8 blocks */             \
         if (c < nrem && r < rows && n > 0) epi.load_t(b, j, i0, n, pret[it]);                        \
       }                                                                                              \
 _Pragma("unroll")                                                                                    \
@@ -875,7 +890,7 @@ _Pragma("unroll")                                                               
         const int r = ((it / CBT) * 8 + lane % 8) * 8;                                               \
         const int j = wc0 + c, i0 = pr0 + r;                                                         \
         int n = min(8, rows - r);                                                                    \
-        if (diag) n = min(n, j - i0);                                                                \
+        if (diag && j - i0 < 8) n = 0;                                                               \
         if (!(c < nrem && r < rows && n > 0)) continue;                                              \
         S v[8];                                                                                      \
 _Pragma("unroll")                                                                                    \
@@ -1296,8 +1311,10 @@ struct EpiBlend {
     if (beta != A(0)) {
       S old[8];
       ld8_use<TO, S>(p, raw, old, kbeg, n, vec);
+      // one fixed rounding (an explicit fma), the same in every kernel
+      // instantiation that blends (single and batched factor updates)
 #pragma unroll
-      for (int k = 0; k < 8; ++k) r[k] = beta * old[k] + alpha * v[k];
+      for (int k = 0; k < 8; ++k) r[k] = fma(beta, old[k], alpha * v[k]);
     } else {
 #pragma unroll
       for (int k = 0; k < 8; ++k) r[k] = alpha * v[k];

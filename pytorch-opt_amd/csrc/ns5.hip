@@ -140,8 +140,10 @@ struct EpiNsSq {
     const int64_t o = (int64_t)b * sd + (int64_t)i * ld + j0;
     S a[8];
     ld8_use<T, S>(Asrc + o, pre, a, kbeg, n, vec);
+    // explicit fused multiply-adds fix the rounding, so it cannot depend on
+    // how the compiler contracts this expression in a given build
 #pragma unroll
-    for (int k = 0; k < 8; ++k) vo[k] = bc * a[k] + cc * v[k] + (i == j0 + k ? ac : A(0));
+    for (int k = 0; k < 8; ++k) vo[k] = fma(cc, v[k], fma(bc, a[k], i == j0 + k ? ac : A(0)));
     st8<T, S>(dst + o, vo, kbeg, n, vec);
   }
   __device__ __forceinline__ void put_t(int b, int j, int i0, const S* v, int n, const PreT&) const {
@@ -266,6 +268,15 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
   hipLaunchKernelGGL(ns_scale_kernel<A>, dim3(nb), dim3(256), 0, stream, partial, eps, scale);
   PTO_LAUNCHED("ns_scale");
 
+  // `out` may alias G exactly or not at all: every path below reads G only
+  // in kernels that end before `out` is written, except the steps == 0
+  // pack, which is tile-local (each element read before it is rewritten
+  // in place) only when the two coincide.
+  const uintptr_t g0 = reinterpret_cast<uintptr_t>(G), g1 = g0 + sizeof(T) * (uintptr_t)(batch * sG);
+  const uintptr_t o0 = reinterpret_cast<uintptr_t>(out), o1 = o0 + sizeof(T) * (uintptr_t)(batch * sG);
+  const bool aliased = g0 < o1 && o0 < g1;
+  PTO_REQUIRE(!aliased || g0 == o0, "newton_schulz_orthogonalize: out partially overlaps G");
+
   if (steps == 0) {  // the normalised input, in the input's layout
     if (launch_pack<T, T, A>(G, rows, cols, cols, sG, scale, out, cols, sG, nullptr, 0, 0, false, nb, stream)) return -1;
     return 0;
@@ -274,7 +285,11 @@ int ns5_t(const T* G, T* out, int64_t batch, int64_t rows, int64_t cols, int64_t
   // X0 = s·X (and, without the QN layout, X0ᵀ), pads zeroed. bf16 inputs
   // that need neither padding nor a transpose skip the copy: the first
   // gram and update read G itself and apply s² and s in their epilogues.
-  const bool direct = QN && !transposed && m == ldm && n == ldn;
+  // The MFMA operand loads are 16-byte accesses, so G must be 16-byte
+  // aligned (a view at an odd element offset is packed instead), and the
+  // first update reads G while its epilogue writes `out` (with one
+  // iteration, the only update), so an aliased call is packed as well.
+  const bool direct = QN && !transposed && m == ldm && n == ldn && (g0 & 15) == 0 && !aliased;
   if (QN && direct) {
     // no pads: X[1] is written in full by the first update
   } else if (QN) {

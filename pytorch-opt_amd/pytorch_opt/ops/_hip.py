@@ -146,6 +146,8 @@ class HipBackend:
             raise OpsArgumentError("newton_schulz_orthogonalize_into: contiguous GPU tensors only")
         if out.shape != G.shape or out.dtype != G.dtype or G.dtype not in _DTYPE_CODE:
             raise OpsArgumentError("newton_schulz_orthogonalize_into: out must match G (float32, float64, bfloat16)")
+        if _overlaps(G, out) and G.data_ptr() != out.data_ptr():
+            raise OpsArgumentError("newton_schulz_orthogonalize_into: out must be G itself or not overlap it")
         rows, cols = G.shape[-2], G.shape[-1]
         batch = math.prod(G.shape[:-2])
         with torch.cuda.device(G.device):
@@ -195,8 +197,10 @@ class HipBackend:
     def kron_factor_update_batched_(self, Ls, Rs, Gs, beta2):
         """kron_factor_update_ on each (L, R, G) of same-shape lists, one launch
         per side for up to KRON_BATCH matrices and KRON_BATCH_BYTES of
-        gradients; each factor gets the bits the single call gives it. The
-        gradients of a launch are stacked into one tensor."""
+        gradients; in float32 and float64 each factor gets the bits the
+        single call gives it (bfloat16 may differ in the last bits: the tile
+        depends on the batch). The gradients of a launch are stacked into
+        one tensor."""
         k = len(Gs)
         if not (len(Ls) == len(Rs) == k):
             raise OpsArgumentError("kron_factor_update_batched_: L, R and G lists differ in length")

@@ -116,6 +116,23 @@ def test_ns5_bf16_coefficient_forms(native_backend, coeffs):
         assert _relfro(_np(got[i]), want) <= 2e-2, (coeffs, i)
 
 
+def test_ns5_bf16_unaligned_view_is_packed(native_backend, hip):
+    """A bf16 view starting 2 bytes into its storage (a flat-buffer slice)
+    with 128-multiple extents: the in-place path's 16-byte loads cannot read
+    it, so it is packed first; through pto_ns5 and the no-alloc entry point
+    alike, both against the oracle."""
+    g = torch.Generator().manual_seed(14)
+    flat = (1e-2 * torch.randn(128 * 256 + 1, generator=g)).bfloat16()
+    Gv = flat.to(DEV)[1:].view(128, 256)
+    assert Gv.data_ptr() % 16 != 0 and Gv.is_contiguous()
+    out = ops.newton_schulz_orthogonalize(Gv)
+    want = oo.ns5(flat[1:].view(128, 256).float().numpy())
+    assert _relfro(_np(out), want) <= 2e-2
+    into = torch.empty_like(Gv)
+    hip.newton_schulz_orthogonalize_into(Gv, into, 5, 3.4445, -4.7750, 2.0315, 1e-7)
+    assert torch.equal(into, out)
+
+
 def test_ns5_semi_orthogonal_bf16(native_backend):
     Q, _ = torch.linalg.qr(torch.randn(512, 256, dtype=torch.float64))
     Q = Q.T.contiguous()  # 256 x 512, rows orthonormal

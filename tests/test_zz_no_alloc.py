@@ -1,7 +1,8 @@
 """The entry point that allocates nothing (pto_ns5_noalloc) against pto_ns5
 on the same inputs: bit-identical outputs on two calls in a row, the second
-smaller (the shared static scratch keeps the first call's contents), and a
-call too large for the scratch refused before any launch."""
+smaller (the shared static scratch keeps the first call's contents), a
+call too large for the scratch refused before any launch, and the aliasing
+rule (out may be G itself, not a partial overlap)."""
 
 import pytest
 import torch
@@ -38,3 +39,24 @@ def test_noalloc_rejects_oversize_call(hip):
     out = torch.empty_like(G)
     with pytest.raises(RuntimeError, match="bytes of scratch"):
         hip.newton_schulz_orthogonalize_into(G, out, 5, *COEFFS, 1e-7)
+
+
+def test_noalloc_in_place_and_partial_overlap(hip):
+    """out = G: the in-place input is packed before anything is written, so
+    one step in place equals pto_ns5 on a packed copy of G; an out that
+    overlaps G only in part is refused."""
+    a, b, c = COEFFS
+    G = _input((256, 384), torch.bfloat16, 7)
+    # the packed path is what an unaligned copy of G takes: compare with it
+    buf = torch.empty(G.numel() + 1, dtype=G.dtype, device=DEV)
+    Gu = buf[1:].view_as(G)
+    Gu.copy_(G)
+    want = hip.newton_schulz_orthogonalize(Gu, 1, a, b, c, 1e-7)
+    X = G.clone()
+    hip.newton_schulz_orthogonalize_into(X, X, 1, a, b, c, 1e-7)
+    torch.cuda.synchronize()
+    assert torch.equal(X, want)
+    store = torch.zeros(2 * 256 * 384, dtype=torch.bfloat16, device=DEV)
+    src, dst = store[:256 * 384].view(256, 384), store[8:8 + 256 * 384].view(256, 384)
+    with pytest.raises(ValueError, match="not overlap"):
+        hip.newton_schulz_orthogonalize_into(src, dst, 1, a, b, c, 1e-7)
