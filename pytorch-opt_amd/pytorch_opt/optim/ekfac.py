@@ -11,8 +11,8 @@ the factors' eigenvalues and no damping this is K-FAC's direction.
 
 Here both rotations are ops.two_sided_product calls (MFMA kernels on a GPU),
 the refresh eighs of same-shape factors share one batched call, and the
-scales live in each module's curvature entry (so they travel with the
-K-FAC checkpoint state).
+scales live in each module's curvature entry; checkpoints carry them in the
+reference's ``"ekfac": {"scales", "scale_decay"}`` entry (:60-72).
 """
 
 from __future__ import annotations
@@ -54,7 +54,7 @@ class EKFAC(KFAC):
 
     def _precondition(self, name: str, V: torch.Tensor) -> torch.Tensor:
         inv = self._inv.get(name)
-        if inv is None:
+        if inv is None or "QG" not in inv:  # (a restored scale alone is no basis)
             raise RuntimeError(f"Missing EKFAC inverse for {name!r}")
         QG, QA = inv["QG"], inv["QA"]
         Vt = ops.two_sided_product(QG, V.to(QG.dtype), QA, transpose_a=True)
@@ -67,11 +67,24 @@ class EKFAC(KFAC):
         lam = self.param_groups[0]["damping"]
         return ops.two_sided_product(QG, Vt / (scale + lam), QA, transpose_b=True).to(V.dtype)
 
-    def _extra_state(self) -> dict:
-        state = super()._extra_state()
-        state["scale_decay"] = self.scale_decay
-        return state
+    def state_dict(self):
+        sd = super().state_dict()
+        scales = {}
+        for name, entry in sd["kfac"]["inv"].items():  # shallow copies of the live entries
+            if "scale" in entry:
+                scales[name] = entry.pop("scale")
+        sd["ekfac"] = {"scales": scales, "scale_decay": self.scale_decay}
+        return sd
 
     def load_state_dict(self, state_dict):
-        self.scale_decay = state_dict.get("kfac", {}).get("scale_decay", self.scale_decay)
-        super().load_state_dict(state_dict)
+        sd = dict(state_dict)
+        extra = sd.pop("ekfac", None)
+        # an earlier version of this module kept scale_decay in the K-FAC entry
+        # and each scale inside its curvature entry, which the K-FAC loader restores
+        self.scale_decay = sd.get("kfac", {}).get("scale_decay", self.scale_decay)
+        super().load_state_dict(sd)
+        if extra is not None:
+            self.scale_decay = extra.get("scale_decay", self.scale_decay)
+            restored = self._on_module_device({n: {"scale": v} for n, v in extra.get("scales", {}).items()})
+            for name, entry in restored.items():
+                self._inv.setdefault(name, {})["scale"] = entry["scale"]

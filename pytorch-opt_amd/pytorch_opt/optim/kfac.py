@@ -10,8 +10,10 @@ training backward every ``stats_every`` steps; every ``inv_every`` steps
 the damped inverses (F + γI)⁻¹ are refreshed with π-split damping
 (:133-158); a module's gradient V (out × in, bias column appended) becomes
 (G + γ_G I)⁻¹·V·(A + γ_A I)⁻¹, then global norm clipping, momentum, weight
-decay and the update (:162-256). Only the empirical Fisher is built; the
-reference's sampled-label Fisher is not on this path.
+decay and the update (:162-256). Curvature comes from the training backward
+(``fisher_mode="empirical"``) or only from update_curvature(outputs),
+an extra backward on labels sampled from the model (``"sampled"``, the
+true Fisher, :27,124-131).
 
 MI355X design:
   * statistics: KronTracker -> ops.gram_update_, one symmetric MFMA launch
@@ -38,7 +40,7 @@ from ..curvature.damping import kfac_factored_damping
 from ..curvature.kron import KronTracker
 from ._common import DiagnosticsMixin, StepTimer, adamw_update, validate_checkpoint_groups, validate_groups
 
-_FISHER_MODES = ("empirical",)
+_FISHER_MODES = ("empirical", "sampled")
 _INVERSE_METHODS = ("eigh", "newton")
 
 
@@ -177,7 +179,7 @@ class KFAC(Optimizer, DiagnosticsMixin):
         self._steps = 0          # optimizer steps taken
         self._inv_stale = 0      # steps since the last inverse refresh
         self._inv: dict[str, dict] = {}
-        self._seen_counts: dict[str, int] = {}  # tracker update counts at the last step
+        self._last_counts: dict[str, int] = {}  # tracker update counts at the last step
         self._arm_tracker()
 
     def _bind_selection(self, model, candidates, regs):
@@ -198,11 +200,28 @@ class KFAC(Optimizer, DiagnosticsMixin):
             raise ValueError("KFAC selection must contain supported, untied module weights and optional biases")
         return modules, with_bias
 
+    def _stats_step(self) -> bool:
+        return self._steps % self.param_groups[0]["stats_every"] == 0
+
     def _arm_tracker(self) -> None:
-        """Statistics are gathered on steps that are multiples of stats_every."""
-        on = self._steps % self.param_groups[0]["stats_every"] == 0
+        """Forward calls are bound on steps that are multiples of stats_every;
+        the training backward feeds the factors on those steps only for the
+        empirical Fisher (the sampled one feeds them from update_curvature)."""
+        on = self._stats_step()
         self.tracker.capture = on
-        self.tracker.enabled = on
+        self.tracker.enabled = on and self.fisher_mode == "empirical"
+
+    def update_curvature(self, outputs: torch.Tensor, kind: str = "categorical",
+                         generator: torch.Generator | None = None) -> None:
+        """fisher_mode="sampled": accumulate the factors from one extra
+        backward of `outputs` (the model's outputs of this step's forward)
+        on labels drawn from the model's predictive distribution
+        (KronTracker.sampled_backward); nothing outside statistics steps."""
+        if self.fisher_mode != "sampled":
+            raise RuntimeError("update_curvature() is only used with fisher_mode='sampled'; "
+                               "empirical mode accumulates from the training backward")
+        if self._stats_step():
+            self.tracker.sampled_backward(outputs, kind=kind, generator=generator)
 
     def set_grad_scale(self, scale: float) -> None:
         """The scale of the next backward's loss (AMP scale / accumulation
@@ -291,13 +310,13 @@ class KFAC(Optimizer, DiagnosticsMixin):
     def _require_fresh_curvature(self, todo) -> None:
         """On a statistics step every module with a gradient must have been
         seen by the hooks (fused or functional calls bypass them)."""
-        stats_step = self._steps % self.param_groups[0]["stats_every"] == 0
+        stats_step = self._stats_step()
         for name, _, _, _ in todo:
-            fresh = self.tracker.updates(name) > self._seen_counts.get(name, 0)
+            fresh = self.tracker.updates(name) > self._last_counts.get(name, 0)
             if name not in self.tracker.factors or (stats_step and not fresh):
                 raise RuntimeError(
-                    f"No K-FAC curvature collected for {name!r}. Check the module hooks: fused or functional "
-                    "projections bypass them.")
+                    f"No K-FAC curvature collected for {name!r}. Check update_curvature and the module hooks: "
+                    "fused or functional projections bypass them.")
 
     def _apply_direction(self, p, d, scale) -> None:
         group = self._group_of[id(p)]
@@ -350,7 +369,7 @@ class KFAC(Optimizer, DiagnosticsMixin):
                 for p in (q for q in group["params"] if q.grad is not None):
                     adamw_update(p, p.grad, self.state[p], group)
                     n_adamw += 1
-            self._seen_counts = self.tracker.update_counts()
+            self._last_counts = self.tracker.update_counts()
             self._steps += 1
             self._arm_tracker()
         mean = lambda k: sum(c[k] for c in conds) / len(conds) if conds else None  # noqa: E731
@@ -360,13 +379,16 @@ class KFAC(Optimizer, DiagnosticsMixin):
         return loss
 
     # ------------------------------------------------------------ checkpoint
+    # The "kfac" entry carries the reference's keys (pytorch_opt/optim/kfac.py:
+    # 260-298), so checkpoints move between the two implementations.
     def _extra_state(self) -> dict:
-        return {"steps": self._steps, "inv_stale": self._inv_stale, "counts": self.tracker.update_counts(),
-                "seen_counts": dict(self._seen_counts), "modules": sorted(self._modules),
-                "bias_modules": sorted(self.tracker.bias_modules), "ema_decay": self.tracker.ema_decay,
-                "grad_scale": self.tracker.grad_scale,
+        return {"steps": self._steps, "inv_stale": self._inv_stale,
                 "factors": {n: dict(f) for n, f in self.tracker.factors.items()},
-                "inv": {n: dict(f) for n, f in self._inv.items()}}
+                "inv": {n: dict(f) for n, f in self._inv.items()},
+                "counts": self.tracker.update_counts(), "last_counts": dict(self._last_counts),
+                "modules": list(self._modules), "bias_modules": sorted(self.tracker.bias_modules),
+                "fisher_mode": self.fisher_mode, "ema_decay": self.tracker.ema_decay,
+                "grad_scale": self.tracker.grad_scale}
 
     def state_dict(self):
         sd = super().state_dict()
@@ -374,21 +396,30 @@ class KFAC(Optimizer, DiagnosticsMixin):
         return sd
 
     def load_state_dict(self, state_dict):
+        """Restores a checkpoint of either implementation. The module lists
+        are compared as sets (the reference writes them in named_modules
+        order); optional keys fall back as the reference's loader does."""
         sd = dict(state_dict)
         extra = sd.pop("kfac", None)
         if extra is None:
             raise ValueError("Checkpoint is missing K-FAC curvature state")
-        if extra["modules"] != sorted(self._modules) or extra["bias_modules"] != sorted(self.tracker.bias_modules):
+        if "modules" in extra and (set(extra["modules"]) != set(self._modules)
+                                   or sorted(extra.get("bias_modules", ())) != sorted(self.tracker.bias_modules)):
             raise ValueError("Checkpoint K-FAC module selection differs from this optimizer")
+        mode = extra.get("fisher_mode", self.fisher_mode)
+        if mode not in _FISHER_MODES:
+            raise ValueError(f"fisher_mode must be one of {_FISHER_MODES}, got {mode!r}")
         validate_checkpoint_groups(self.param_groups, sd["param_groups"])
         super().load_state_dict(sd)
         self._steps, self._inv_stale = int(extra["steps"]), int(extra["inv_stale"])
-        self.tracker.ema_decay = extra["ema_decay"]
-        self.tracker.set_grad_scale(extra["grad_scale"])
-        self.tracker.restore_counts(extra["counts"])
-        self._seen_counts = dict(extra["seen_counts"])
+        self.fisher_mode = mode
+        self.tracker.ema_decay = extra.get("ema_decay", self.tracker.ema_decay)
+        self.tracker.set_grad_scale(extra.get("grad_scale", 1.0))
         self.tracker.factors = self._on_module_device(extra["factors"])
         self._inv = self._on_module_device(extra["inv"])
+        self.tracker.restore_counts(extra["counts"])
+        # "seen_counts": the key an earlier version of this module wrote
+        self._last_counts = dict(extra.get("last_counts", extra.get("seen_counts", extra["counts"])))
         self._arm_tracker()
 
     def _on_module_device(self, tree: dict) -> dict:
