@@ -1,6 +1,9 @@
 """The backend switch contract of the reference's pytorch_opt/ops/__init__.py
-(tests/test_ops_dispatch.py and the load/skip behaviour of
-tests/test_ops_native_parity.py in the reference)."""
+(the behaviour its tests/test_ops_dispatch.py and the load/skip logic of
+tests/test_ops_native_parity.py check): states and refusals of the switch,
+the pure-torch maths when no library is loaded (against closed forms),
+load failures that warn and degrade, CPU tensors under a loaded backend,
+and argument errors raised as both ValueError and RuntimeError."""
 
 import warnings
 
@@ -19,33 +22,48 @@ def _restore():
     ops.set_backend("auto")
 
 
-def test_default_backend():
+def test_switch_states_and_refusals():
+    """The switch starts at "auto"; "reference" and "auto" can always be
+    chosen, "native" only once a library is loaded, anything else never; a
+    refused switch leaves the selection as it was."""
+    assert ops.get_backend() == "auto"
+    ops._NATIVE = None
+    ops.set_backend("reference")
+    refusals = [("native", RuntimeError, "native backend not loaded"), ("cuda", ValueError, "backend must be one of"),
+                ("Reference", ValueError, "backend must be one of")]
+    for name, exc, message in refusals:
+        with pytest.raises(exc, match=message):
+            ops.set_backend(name)
+        assert ops.get_backend() == "reference"
+    ops.set_backend("auto")
     assert ops.get_backend() == "auto"
 
 
-def test_auto_without_native_matches_reference(device):
+def _known_spectrum(n, seed, device):
+    """Q·diag(λ)·Qᵀ with Q from QR of a seeded Gaussian and λ in [0.2, 3]."""
+    g = torch.Generator().manual_seed(seed)
+    Q, _ = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))
+    lam = 0.2 + 2.8 * torch.rand(n, generator=g, dtype=torch.float64)
+    return Q, lam
+
+
+def test_unloaded_auto_computes_closed_forms(device):
+    """With no library loaded, "auto" runs the pure-torch maths on any device:
+    the inverse 4th root of Q·diag(λ)·Qᵀ is Q·diag(λ^-1/4)·Qᵀ, and NS5 of a
+    matrix with orthonormal singular vectors keeps them, mapping each
+    normalised singular value through five quintic steps."""
     ops._NATIVE = None
-    A = torch.randn(5, 5, device=device)
-    A = A @ A.T + 0.1 * torch.eye(5, device=device)
-    assert torch.allclose(ops.inverse_matrix_root(A, 4), ops_ref.inverse_matrix_root(A, 4))
-    G = torch.randn(4, 6, device=device)
-    assert torch.allclose(ops.newton_schulz_orthogonalize(G), ops_ref.newton_schulz_orthogonalize(G))
-
-
-def test_reference_backend_explicit():
-    ops.set_backend("reference")
-    assert ops.get_backend() == "reference"
-
-
-def test_unknown_backend_rejected():
-    with pytest.raises(ValueError, match="backend"):
-        ops.set_backend("bogus")
-
-
-def test_native_requires_load():
-    ops._NATIVE = None
-    with pytest.raises(RuntimeError, match="native backend not loaded"):
-        ops.set_backend("native")
+    Q, lam = _known_spectrum(6, 31, device)
+    A = ((Q * lam) @ Q.T).float().to(device)
+    want = (Q * lam ** -0.25) @ Q.T
+    assert float((ops.inverse_matrix_root(A, 4).double().cpu() - want).abs().max()) < 1e-5
+    s = torch.tensor([1.7, 0.9, 0.4], dtype=torch.float64)
+    U, V = Q[:, :3], _known_spectrum(5, 32, device)[0][:, :3]
+    x = s / s.norm()
+    for _ in range(5):
+        x = 3.4445 * x - 4.7750 * x ** 3 + 2.0315 * x ** 5
+    out = ops.newton_schulz_orthogonalize(((U * s) @ V.T).float().to(device))
+    assert float((out.double().cpu() - (U * x) @ V.T).abs().max()) < 1e-5
 
 
 def test_load_failure_warns_and_degrades(monkeypatch, tmp_path):
