@@ -202,10 +202,14 @@ def bench_roots(torch, hip, dev, cpu):
         X2 = Xd @ Xd
         M = A.double() + 1e-6 * torch.eye(n, dtype=torch.float64, device=dev)
         resid = float(((X2 @ X2) @ M - torch.eye(n, dtype=torch.float64, device=dev)).norm() / n ** 0.5)
-        it_flops = 4 * n ** 3 + 2 * n * n * (n + 1)  # LAWN-41 count per iteration: X·Mi, Mi⁴·Mk; Mi², Mi⁴
+        # LAWN-41 count per iteration, as the kernels compute it: X·Mi, Mi², Mi⁴ and
+        # Mi⁴·Mk are all products of commuting polynomials in M, so each is a
+        # symmetric product on upper tiles, n²(n+1) flops
+        it_flops = 4 * n * n * (n + 1)
+        tflops = iters * it_flops / wall / 1e12
         entry = {"ms": round(wall * 1e3, 2), "iterations": iters, "ms_per_iter": round(wall * 1e3 / max(iters, 1), 3),
-                 "residual": float(f"{resid:.4e}"),
-                 "tflops": round(iters * it_flops / wall / 1e12, 2)}
+                 "residual": float(f"{resid:.4e}"), "alg_flops_per_iter": it_flops,
+                 "tflops": round(tflops, 2), "frac_fp32_peak": round(tflops / PEAK["fp32"], 4)}
         gold = golden_roots.get(str(n))
         if gold is not None:  # the numpy oracle's float32 run, tests/golden/root_config4.json
             entry["oracle_residual"] = float(f"{gold['residual']:.4e}")
@@ -666,7 +670,10 @@ def main():
         "config": {"workload": "batched NS5 bf16: 32 x 4096x4096 + 32 x 4096x11008, 5 quintic iterations",
                    "alg_flops_per_step": flops_step, "pct_bf16_mfma_peak": round(100 * value / PEAK["bf16"], 2)},
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK["bf16"], "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK["bf16"], 4), "traffic": load_traffic()},
+                     "frac": round(achieved / PEAK["bf16"], 4), "traffic": load_traffic(),
+                     "traffic_source": "not measured in this run: bytes per ns5_update launch read from "
+                                       "profiles/ns5_bf16_traffic.json, the digest of two rocprofv3 --pmc passes "
+                                       "(FETCH_SIZE, WRITE_SIZE) of bench.py --traffic-probe scaled by a 1 GiB copy"},
         "kernels": kinds,
         "single_4096": {"ms": round(single_ms, 3), "tflops": round(single_tflops, 2),
                         "pct_bf16_mfma_peak": round(100 * single_tflops / PEAK["bf16"], 2)},
