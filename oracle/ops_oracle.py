@@ -22,10 +22,12 @@ Pinning (tests/test_oracle.py):
   coupled_newton       values through inverse_root's closed forms; the stop
                        rule's iteration count is pinned in float64 (where
                        convergence, not rounding noise, ends the loop) by the
-                       iteration bound of the quadratic phase; the exact
-                       float32 stopping iteration is noise-driven: "parity
-                       unpinned" for that count (the reference ships no
-                       golden vectors)
+                       iteration bound of the quadratic phase; in float32,
+                       run with the root kernels' product order
+                       (gemm_emu.c as ``matmul``), its iterate, err sequence
+                       and iteration count equal the kernels' bit for bit
+                       on the config-4 inputs (tests/test_root_emulated.py),
+                       which pins both sides against each other
   gram_update          brute-force sum of outer products, clone/EMA/mean
   precond_apply        associativity / brute force in float64
   two_sided_product    orthogonal round trip Q·(QᵀXQ)·Qᵀ = X, permutation
@@ -100,12 +102,13 @@ def kron_factor_update(L, R, G, beta2=1.0, dtype=None):
     return L * bb + aa * left, R * bb + aa * right
 
 
-def coupled_newton(M, p, max_iter=100, tol=1e-10, matmul=np.matmul):
+def coupled_newton(M, p, max_iter=100, tol=1e-10, matmul=np.matmul, errors=None):
     """Coupled Newton for M^(-1/p) — pytorch_opt/ops/reference.py:17-40.
 
     Returns (X, iterations executed). M is [..., n, n] in the root dtype.
     ``matmul`` computes every product (a test can change the summation
-    order; the default is numpy's BLAS).
+    order; the default is numpy's BLAS). ``errors``, a list, receives each
+    iteration's err = max|Mk − I|.
     """
     dt = M.dtype.type
     n = M.shape[-1]
@@ -124,6 +127,8 @@ def coupled_newton(M, p, max_iter=100, tol=1e-10, matmul=np.matmul):
         X = matmul(X, Mi)
         Mk = matmul(matrix_power(Mi, p, matmul), Mk)
         err = np.max(np.abs(Mk - eye))
+        if errors is not None:
+            errors.append(float(err))
         if good_err is not None and err > good_err * dt(1.2):
             return good, iters
         good, good_err = X, err
@@ -152,11 +157,11 @@ def matrix_power(A, p, matmul=np.matmul):
 
 
 def inverse_root(A, p, damping=0.0, method="auto", root_dtype=np.float64, max_iter=100, tol=1e-10,
-                 matmul=np.matmul):
+                 matmul=np.matmul, errors=None):
     """(A + damping·I)^(-1/p) — pytorch_opt/ops/reference.py:43-68.
 
     Returns (root in the input dtype, iterations; 0 for eigh). ``matmul``
-    as in coupled_newton.
+    and ``errors`` as in coupled_newton.
     """
     if int(p) != p or p < 1:
         raise ValueError(f"p must be a positive integer, got {p}")
@@ -167,7 +172,7 @@ def inverse_root(A, p, damping=0.0, method="auto", root_dtype=np.float64, max_it
     if damping:
         M = M + root_dtype(damping) * np.eye(M.shape[-1], dtype=root_dtype)
     if method == "newton":
-        X, iters = coupled_newton(M, int(p), max_iter, tol, matmul)
+        X, iters = coupled_newton(M, int(p), max_iter, tol, matmul, errors)
     else:
         lam, V = np.linalg.eigh(M)
         lam = np.maximum(lam, 1e-30)

@@ -73,6 +73,14 @@ struct Bits<double> {
   __device__ static U of(double v) { return (U)__double_as_longlong(v); }
 };
 
+// Separately rounded product and sum (never contracted into one fused
+// operation), so the elementwise steps round as the reference's torch ops
+// do: M = 0.5·(A + Aᵀ) then + damping·I; Mi = (1 − α)·I + α·Mk.
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ double mul_rn(double a, double b) { return __dmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ double add_rn(double a, double b) { return __dadd_rn(a, b); }
+
 // M = sym(A) + damping·I in precision R, [n][ld] with zeroed pads.
 template <typename TI, typename R>
 __global__ void __launch_bounds__(256) root_sym_kernel(const TI* __restrict__ A, int64_t n, int64_t sA, R damping,
@@ -95,8 +103,8 @@ __global__ void __launch_bounds__(256) root_sym_kernel(const TI* __restrict__ A,
     if (r >= n || c >= ld) continue;
     R v = R(0);
     if (c < n) {
-      v = R(0.5) * (t1[rr][tx] + t2[tx][rr]);
-      if (r == c && damping != R(0)) v = v + damping;
+      v = mul_rn(R(0.5), add_rn(t1[rr][tx], t2[tx][rr]));
+      if (r == c && damping != R(0)) v = add_rn(v, damping);
     }
     Mb[r * ld + c] = v;
   }
@@ -129,9 +137,9 @@ __global__ void root_init_kernel(const R* __restrict__ M, int64_t n, int64_t ld,
     R x = R(0), mk = R(0), mi = R(0);
     if (c < n) {
       mk = M[o] * z[b];
-      mi = alpha * mk;
+      mi = mul_rn(alpha, mk);
       if (r == c) {
-        mi = c1 + mi;
+        mi = add_rn(c1, mi);
         x = xs[b];
       }
     }
@@ -175,9 +183,9 @@ struct EpiMk {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       R d = v[k];
-      mi[k] = alpha * v[k];
+      mi[k] = mul_rn(alpha, v[k]);
       if (row == c0 + k) {
-        mi[k] = c1 + mi[k];
+        mi[k] = add_rn(c1, mi[k]);
         d = v[k] - R(1);
       }
       if (k >= kbeg && k < n) {
