@@ -19,8 +19,10 @@ the same workload, and secondary figures:
                 2048 / 4096 with λ log-uniform in [1e-6, 1], ε = 1e-6;
   optimizer     Muon + Shampoo steps on the synthetic 12-layer d=2048
                 parameter set (40 steps each), SOAP on its 48 attention
-                matrices (one refresh period, 10 steps), with the CPU
-                path's per-step estimate from a bounded sample;
+                matrices (one refresh period, 10 steps; and with
+                basis_refresh="power", whose refreshes after the first are
+                one subspace-iteration step, timed at step 20), with the
+                CPU path's per-step estimate from a bounded sample;
   kfac          K-FAC and EKFAC steps on 4 x Linear(2048, 2048), 8192
                 tokens (one inv_every = 10 period), with a CPU estimate.
 """
@@ -293,11 +295,11 @@ def bench_optimizer(torch, ops, hip, dev, steps, cpu):
         return Shampoo([{"params": attn}, {"params": rest, "use_preconditioner": False, "lr": 3e-4}],
                        max_preconditioner_dim=4096, precondition_frequency=20, graft="adagrad")
 
-    def make_soap(P):
+    def make_soap(P, basis_refresh="eigh"):
         attn = [P[n] for n, _, _ in mats if kind[n] == "attn"]
         rest = [P[n] for n, _, _ in mats if kind[n] == "mlp"] + [P[n] for n, _ in vecs] + [P["emb"]]
         return SOAP([{"params": attn}, {"params": rest, "use_preconditioner": False}], lr=3e-3,
-                    max_preconditioner_dim=4096, precondition_frequency=10)
+                    max_preconditioner_dim=4096, precondition_frequency=10, basis_refresh=basis_refresh)
 
     m_mean, _ = run(make_muon)
     s_mean, s_per = run(make_shampoo)
@@ -308,6 +310,14 @@ def bench_optimizer(torch, ops, hip, dev, steps, cpu):
     out["soap_plain_step_ms"] = round(1e3 * sum(soap_per[1:]) / 9, 2)
     out["soap_step_ms"] = round(1e3 * sum(soap_per) / 10, 2)
     out["soap_plain_alg_tflops"] = round(48 * soap_matrix_flops(2048, 2048) / (sum(soap_per[1:]) / 9) / 1e12, 2)
+    # SOAP(basis_refresh="power"): eigh at step 0, then every refresh is
+    # one subspace-iteration step per factor (F·Q, shifted CholeskyQR3 in
+    # float64); timed at its second such refresh, step 20 (the first pays
+    # the process's one-time setup of torch's batched GEMM and
+    # factorisations), over the period steps 11..20
+    _, pw_per = run(lambda P: make_soap(P, "power"), 21)
+    out["soap_power_refresh_step_ms"] = round(pw_per[20] * 1e3, 1)
+    out["soap_power_step_ms"] = round(1e3 * sum(pw_per[11:21]) / 10, 2)
     refresh = [s_per[i] for i in range(steps) if i % 20 == 0]
     plain = [s_per[i] for i in range(steps) if i % 20 != 0]
     out["muon_step_ms"] = round(m_mean * 1e3, 2)

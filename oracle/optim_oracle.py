@@ -91,8 +91,25 @@ def shampoo_matrix_step(p, g, L, R, L_root, R_root, graft_acc, step, factor_upda
     return p, L, R, L_root, R_root, graft_acc
 
 
+def soap_power_basis(F, Q):
+    """One subspace-iteration step of a SOAP eigenbasis from its current
+    estimate Q (the power-iteration refresh of Vyas et al., "SOAP", 2024,
+    Algorithm 4; the library's SOAP(basis_refresh="power"), which has no
+    counterpart in the reference): the columns of Q ordered by descending
+    Rayleigh quotient diag(Qᵀ·F·Q) (ties in index order), then the
+    orthonormal factor of W = F·Q whose R has a positive diagonal. Here by
+    Householder QR (numpy, float64) with the signs of R's diagonal moved
+    into Q; the library computes the same factor by shifted CholeskyQR3.
+    Returned in F's dtype."""
+    Fd, Qd = F.astype(np.float64), Q.astype(np.float64)
+    W = Fd @ Qd
+    order = np.argsort(-np.einsum("ij,ij->j", Qd, W), kind="stable")
+    Qn, R = np.linalg.qr(W[:, order])
+    return (Qn * np.where(np.diag(R) < 0, -1.0, 1.0)).astype(F.dtype)
+
+
 def soap_matrix_step(p, g, state, lr=3e-3, betas=(0.95, 0.95), shampoo_beta=0.95, eps=1e-8,
-                     precondition_frequency=10, weight_decay=0.0):
+                     precondition_frequency=10, weight_decay=0.0, basis_refresh="eigh"):
     """One SOAP update of a selected matrix (pytorch_opt/optim/soap.py:48-66,
     :80-125): factor EMA, eigenbasis refresh every `precondition_frequency`
     steps with the second moment transported through the squared
@@ -114,8 +131,12 @@ def soap_matrix_step(p, g, state, lr=3e-3, betas=(0.95, 0.95), shampoo_beta=0.95
                   exp_avg_sq=np.zeros_like(g2), step=0)
     st["L"], st["R"] = oo.kron_factor_update(st["L"], st["R"], g2, shampoo_beta)
     if st["step"] % precondition_frequency == 0:
-        QL = np.linalg.eigh(st["L"].astype(np.float64))[1].astype(dt)
-        QR = np.linalg.eigh(st["R"].astype(np.float64))[1].astype(dt)
+        if basis_refresh == "power" and "Q_L" in st:
+            QL = soap_power_basis(st["L"], st["Q_L"])
+            QR = soap_power_basis(st["R"], st["Q_R"])
+        else:
+            QL = np.linalg.eigh(st["L"].astype(np.float64))[1].astype(dt)
+            QR = np.linalg.eigh(st["R"].astype(np.float64))[1].astype(dt)
         if "Q_L" in st:
             CL = st["Q_L"].T @ QL
             CR = st["Q_R"].T @ QR

@@ -806,6 +806,48 @@ def test_soap_step_at_size_vs_oracle(native_backend):
     assert np.abs(p.detach().cpu().numpy() - want_p).max() < 5e-5
 
 
+def test_soap_power_refresh_at_size_vs_oracle(native_backend):
+    """SOAP(basis_refresh="power") on a 512x768 fp32 matrix: the step that
+    runs the second refresh (one subspace-iteration step from the step-0
+    bases: F·Q, three float64 Grams on the library's fp64 symmetric
+    kernel, Choleskys and triangular solves) vs the oracle's Householder
+    restatement from the same state: the new bases, the transported second
+    moment and the parameters. The gradients are (U·diag(a))·Z·(V·diag(b))ᵀ
+    with Z random and a, b geometric (0.997^i, 0.998^j), so both factors'
+    eigenvalues spread over a factor ~20: neighbouring Rayleigh quotients
+    then differ by far more than float32 rounding, and the refresh's column
+    order is the same on both sides."""
+    from oracle import optim_oracle as oopt
+    from pytorch_opt import SOAP
+
+    torch.manual_seed(45)
+    U = torch.linalg.qr(torch.randn(512, 512, device=DEV))[0] * 0.997 ** torch.arange(512, device=DEV)
+    V = torch.linalg.qr(torch.randn(768, 768, device=DEV))[0] * 0.998 ** torch.arange(768, device=DEV)
+
+    def grad():
+        return (U @ torch.randn(512, 768, device=DEV) @ V.T).contiguous()
+
+    p = torch.nn.Parameter(0.1 * torch.randn(512, 768, device=DEV))
+    kw = dict(lr=1e-2, betas=(0.9, 0.95), shampoo_beta=0.9, precondition_frequency=4)
+    opt = SOAP([p], max_preconditioner_dim=1024, basis_refresh="power", **kw)
+    for _ in range(4):  # refresh at step 0 (eigh); both factors full rank by step 4
+        p.grad = grad()
+        opt.step()
+    g = grad()
+    p.grad = g
+    st = {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in opt.state[p].items() if k != "stale"}
+    want_p, want_st = oopt.soap_matrix_step(p.detach().cpu().numpy(), g.cpu().numpy(), st,
+                                            basis_refresh="power", **kw)
+    opt.step()
+    for k in ("Q_L", "Q_R"):
+        Q = opt.state[p][k].double()
+        assert float((Q.T @ Q - torch.eye(Q.shape[0], device=DEV, dtype=torch.float64)).abs().max()) < 1e-5, k
+        np.testing.assert_allclose(Q.cpu().numpy(), want_st[k], atol=5e-4, err_msg=k)
+    np.testing.assert_allclose(opt.state[p]["exp_avg_sq"].cpu().numpy(), want_st["exp_avg_sq"], rtol=1e-3,
+                               atol=1e-9)
+    assert np.abs(p.detach().cpu().numpy() - want_p).max() < 5e-5
+
+
 def test_muon_step_at_size_vs_oracle(native_backend):
     """Two Muon steps of a 1024x4096 fp32 matrix (Nesterov momentum, weight
     decay, spectral lr factor), each vs the numpy oracle from the same state."""

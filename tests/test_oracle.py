@@ -409,6 +409,73 @@ def test_soap_oracle_fixed_basis_is_rotated_adam():
     assert not np.allclose(p, p0 + QL @ z_bad @ QR.T, atol=1e-4)
 
 
+def _spd_with_spectrum(lam, rng):
+    V = _orth(len(lam), rng)
+    return (V * lam) @ V.T, V
+
+
+def test_soap_power_basis_closed_form_and_qr_property():
+    """From an exact eigenbasis (columns in any order and signs), one step
+    returns that basis with the columns in descending eigenvalue order and
+    each sign fixed by R's positive diagonal (W = Q·diag(λ) is already
+    orthogonal, so R = diag(λ) and Q_new = the sorted columns, signs as
+    given). From any basis, Q_newᵀ·Q_new = I and Q_newᵀ·W is upper
+    triangular with a positive diagonal, W the sorted F·Q."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(41)
+    lam = np.array([5.0, 0.5, 3.0, 1.0, 2.0, 0.25])
+    F, V = _spd_with_spectrum(lam, rng)
+    signs = np.array([1, -1, -1, 1, 1, -1])
+    perm = np.array([3, 0, 5, 1, 4, 2])
+    Q = (V * signs)[:, perm]
+    got = oopt.soap_power_basis(F, Q)
+    want_order = np.argsort(-lam)
+    np.testing.assert_allclose(got, (V * signs)[:, want_order], atol=1e-12)
+    Q0 = _orth(6, rng)
+    Qn = oopt.soap_power_basis(F, Q0)
+    np.testing.assert_allclose(Qn.T @ Qn, np.eye(6), atol=1e-12)
+    W = F @ Q0
+    W = W[:, np.argsort(-np.einsum("ij,ij->j", Q0, W), kind="stable")]
+    R = Qn.T @ W
+    np.testing.assert_allclose(np.tril(R, -1), 0, atol=1e-12)
+    assert np.all(np.diag(R) > 0)
+
+
+def test_soap_power_basis_converges_to_eigh():
+    """Repeated steps on a fixed factor with a separated spectrum converge
+    to its eigenbasis (simultaneous iteration): Q_newᵀ·F·Q_new becomes
+    diagonal with numpy's eigenvalues in descending order. The planted slip
+    (ascending order, so Gram-Schmidt starts from the smallest direction)
+    does not converge."""
+    from oracle import optim_oracle as oopt
+
+    rng = np.random.default_rng(42)
+    n = 24
+    lam = 1.6 ** -np.arange(n)
+    F, _ = _spd_with_spectrum(lam, rng)
+    Q = _orth(n, rng)
+    for _ in range(120):
+        Q = oopt.soap_power_basis(F, Q)
+    D = Q.T @ F @ Q
+    off = np.linalg.norm(D - np.diag(np.diag(D))) / np.linalg.norm(D)
+    assert off < 1e-9, off
+    np.testing.assert_allclose(np.diag(D), np.sort(np.linalg.eigvalsh(F))[::-1], rtol=1e-9)
+
+    def ascending(F, Q):
+        W = F @ Q
+        Qn, R = np.linalg.qr(W[:, np.argsort(np.einsum("ij,ij->j", Q, W), kind="stable")])
+        return Qn * np.where(np.diag(R) < 0, -1.0, 1.0)
+
+    Qb = np.linalg.eigh(F)[1]  # start from the exact basis, ascending as eigh returns it
+    Qb = Qb @ _orth(n, rng) * 1e-3 + Qb  # a small perturbation
+    Qb = np.linalg.qr(Qb)[0]
+    for _ in range(120):
+        Qb = ascending(F, Qb)
+    Db = Qb.T @ F @ Qb
+    assert np.linalg.norm(Db - np.diag(np.diag(Db))) / np.linalg.norm(Db) > 1e-3
+
+
 def test_kfac_direction_is_the_dense_kronecker_solve():
     """vec(G⁻¹·V·A⁻¹) = (A ⊗ G)⁻¹·vec(V) with column-major vec (the
     reference's orientation test, tests/test_kfac.py:9-20); the swapped

@@ -8,7 +8,11 @@ kernels (factor updates, eigenbasis rotations, second-moment transport):
   gradients Q_Lᵀ·G·Q_R and rotated back;
 * vectors take the AdamW fallback (vs the numpy oracle);
 * teacher-forced steps against the numpy oracle across refreshes, and a
-  small regression that converges.
+  small regression that converges;
+* the opt-in power refresh (basis_refresh="power"): eigh until the second
+  refresh, bit for bit; teacher-forced bases and steps against the oracle's
+  Householder restatement; convergence to the eigenbasis of a fixed factor;
+  shifted CholeskyQR3 on a matrix of condition number 1e10.
 """
 
 import numpy as np
@@ -160,6 +164,99 @@ def test_teacher_forced_vs_oracle(device):
         np.testing.assert_allclose(opt.state[p]["exp_avg_sq"].cpu().numpy(), want_st["exp_avg_sq"], rtol=1e-3,
                                    atol=1e-9, err_msg=f"step {t}")
     assert opt.state[p]["step"] == 6
+
+
+def test_power_refresh_is_eigh_until_its_second_refresh(device):
+    """basis_refresh="power" takes eigh for each factor's first basis, so a
+    run equals the default's bit for bit through the steps before the
+    second refresh, and departs from it there."""
+    torch.manual_seed(5)
+    p0 = 0.1 * torch.randn(24, 40, device=device)
+    grads = [torch.randn(24, 40, device=device) for _ in range(5)]
+    runs = {}
+    for mode in ("eigh", "power"):
+        p = nn.Parameter(p0.clone())
+        opt = SOAP([p], precondition_frequency=3, basis_refresh=mode)
+        runs[mode] = []
+        for g in grads:
+            p.grad = g.clone()
+            opt.step()
+            runs[mode].append(p.detach().clone())
+    for t in range(3):
+        assert torch.equal(runs["eigh"][t], runs["power"][t]), t
+    assert not torch.equal(runs["eigh"][3], runs["power"][3])
+    with pytest.raises(ValueError, match="basis_refresh"):
+        SOAP([nn.Parameter(p0.clone())], basis_refresh="qr")
+
+
+def test_power_refresh_teacher_forced_vs_oracle(device):
+    """SOAP(basis_refresh="power") on a 36x36 matrix (both factors full
+    rank from the first step), refreshing every 2 steps, against the
+    oracle's power refresh (Householder QR in float64, independent of the
+    CholeskyQR3 here) started from the state each step begins in: the new
+    bases after each refresh and the parameters after every step from
+    step 1. (Step 0's bases are the eigenvectors of G·Gᵀ and Gᵀ·G, so
+    Q_Lᵀ·G·Q_R is diagonal up to rounding, and Adam's first step, the sign
+    of each rotated entry, takes the sign of that rounding noise.)"""
+    torch.manual_seed(6)
+    p = nn.Parameter(0.1 * torch.randn(36, 36, device=device))
+    kw = dict(lr=1e-2, betas=(0.9, 0.95), shampoo_beta=0.9, precondition_frequency=2)
+    opt = SOAP([p], max_preconditioner_dim=128, basis_refresh="power", **kw)
+    for t in range(7):
+        g = torch.randn(36, 36, device=device)
+        p.grad = g
+        st_np = {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in opt.state[p].items() if k != "stale"}
+        want_p, want_st = oopt.soap_matrix_step(p.detach().cpu().numpy(), g.cpu().numpy(), st_np,
+                                                basis_refresh="power", **kw)
+        opt.step()
+        if t % 2 == 0 and t > 0:  # power refreshes (step 0's eigh may pick other signs on a GPU)
+            for k in ("Q_L", "Q_R"):
+                np.testing.assert_allclose(opt.state[p][k].cpu().numpy(), want_st[k], atol=2e-4, err_msg=f"{k} {t}")
+        if t > 0:
+            np.testing.assert_allclose(p.detach().cpu().numpy(), want_p, atol=2e-5, err_msg=f"step {t}")
+
+
+def test_power_refresh_converges_on_a_fixed_factor(device):
+    """Refreshed against one fixed factor with eigenvalues 0.8^i, the
+    library's bases converge to its eigenbasis: Qᵀ·F·Q diagonal to 1e-5 of
+    its norm, the diagonal = the eigenvalues in descending order."""
+    n = 48
+    g = torch.Generator().manual_seed(7)
+    V = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))[0]
+    lam = 0.8 ** torch.arange(n, dtype=torch.float64)
+    F = ((V * lam) @ V.T).float().to(device)
+    Q = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))[0].float().to(device)
+    opt = SOAP([nn.Parameter(torch.zeros(n, n, device=device))], basis_refresh="power")
+    for _ in range(150):
+        Q = opt._power_bases([F], [Q])[0]
+    D = Q.double().T @ F.double() @ Q.double()
+    d = torch.diagonal(D)
+    assert float((D - torch.diag(d)).norm() / D.norm()) < 1e-5
+    np.testing.assert_allclose(d.cpu().numpy(), lam.numpy(), atol=1e-6)
+
+
+def test_cholqr3_on_an_ill_conditioned_matrix(device):
+    """Shifted CholeskyQR3 in float64 on W of condition number 1e10 (past
+    what plain CholeskyQR handles, cond² > 1/u): QᵀQ = I and W = Q·R with R
+    upper triangular and a positive diagonal, R = QᵀW; its Q equals
+    numpy's Householder factor with R's signs made positive on the leading
+    (well-conditioned) columns."""
+    rng = np.random.default_rng(8)
+    m, k = 64, 40
+    U = np.linalg.qr(rng.standard_normal((m, k)))[0]
+    Vt = np.linalg.qr(rng.standard_normal((k, k)))[0]
+    W = (U * np.logspace(0, -10, k)) @ Vt
+    Q, ok = SOAP._cholqr3(torch.from_numpy(W).to(device)[None])
+    assert bool(ok[0])
+    Q = Q[0].cpu().numpy()
+    np.testing.assert_allclose(Q.T @ Q, np.eye(k), atol=1e-12)
+    R = Q.T @ W
+    np.testing.assert_allclose(np.tril(R, -1), 0, atol=1e-12)
+    assert np.all(np.diag(R) > 0)
+    np.testing.assert_allclose(Q @ R, W, atol=1e-14)
+    Qh, Rh = np.linalg.qr(W)
+    Qh = Qh * np.where(np.diag(Rh) < 0, -1.0, 1.0)
+    np.testing.assert_allclose(Q[:, :10], Qh[:, :10], atol=1e-9)
 
 
 def test_oversized_matrix_raises(device):
