@@ -12,7 +12,8 @@ kernels (factor updates, eigenbasis rotations, second-moment transport):
 * the opt-in power refresh (basis_refresh="power"): eigh until the second
   refresh, bit for bit; teacher-forced bases and steps against the oracle's
   Householder restatement; convergence to the eigenbasis of a fixed factor;
-  shifted CholeskyQR3 on a matrix of condition number 1e10.
+  shifted CholeskyQR3 on a matrix of condition number 1e10; the eigh
+  fallback where a CholeskyQR fails; stacked refreshes of mixed shapes.
 """
 
 import numpy as np
@@ -257,6 +258,56 @@ def test_cholqr3_on_an_ill_conditioned_matrix(device):
     Qh, Rh = np.linalg.qr(W)
     Qh = Qh * np.where(np.diag(Rh) < 0, -1.0, 1.0)
     np.testing.assert_allclose(Q[:, :10], Qh[:, :10], atol=1e-9)
+
+
+def test_power_refresh_falls_back_to_eigh(device, monkeypatch):
+    """Where the CholeskyQR reports failure, that matrix's refresh is eigh:
+    with every CholeskyQR failing, basis_refresh="power" runs exactly the
+    default's steps (two parameters of different shapes, so two stacks)."""
+    torch.manual_seed(9)
+    shapes = [(12, 20), (16, 16)]
+    p0 = [0.1 * torch.randn(s, device=device) for s in shapes]
+    grads = [[torch.randn(s, device=device) for s in shapes] for _ in range(5)]
+
+    def failing(W):
+        return W, torch.zeros(W.shape[0], dtype=torch.bool, device=W.device)
+
+    runs = {}
+    for mode in ("eigh", "power"):
+        ps = [nn.Parameter(x.clone()) for x in p0]
+        opt = SOAP(ps, precondition_frequency=2, basis_refresh=mode)
+        if mode == "power":
+            monkeypatch.setattr(SOAP, "_cholqr3", staticmethod(failing))
+        for gs in grads:
+            for p, g in zip(ps, gs):
+                p.grad = g.clone()
+            opt.step()
+        runs[mode] = [p.detach().clone() for p in ps]
+    for a, b in zip(runs["eigh"], runs["power"]):
+        assert torch.equal(a, b)
+
+
+def test_power_refresh_mixed_shapes_match_single_parameter_runs(device):
+    """Same-shape factors are stacked into one refresh; each parameter's
+    trajectory equals a run of that parameter alone, up to the rounding of
+    stacked against single GEMMs and eighs."""
+    torch.manual_seed(10)
+    shapes = [(12, 20), (12, 20), (20, 12)]
+    p0 = [0.1 * torch.randn(s, device=device) for s in shapes]
+    grads = [[torch.randn(s, device=device) for s in shapes] for _ in range(6)]
+    ps = [nn.Parameter(x.clone()) for x in p0]
+    opt = SOAP(ps, precondition_frequency=2, basis_refresh="power")
+    for gs in grads:
+        for p, g in zip(ps, gs):
+            p.grad = g.clone()
+        opt.step()
+    for i in range(len(shapes)):
+        q = nn.Parameter(p0[i].clone())
+        solo = SOAP([q], precondition_frequency=2, basis_refresh="power")
+        for gs in grads:
+            q.grad = gs[i].clone()
+            solo.step()
+        torch.testing.assert_close(ps[i].detach(), q.detach(), rtol=0, atol=2e-5, msg=f"parameter {i}")
 
 
 def test_oversized_matrix_raises(device):
