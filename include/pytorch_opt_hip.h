@@ -64,8 +64,12 @@ int pto_ns5(const void* G, void* out, int dtype, int64_t batch, int64_t rows, in
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation). It has no counterpart in the
  * reference. The workspace is a static 256 MiB device array in the library,
- * one per GPU, allocated when the library's code is loaded on that GPU and
- * held until the process ends; a call whose pto_ns5_workspace_bytes exceeds
+ * one per GPU. It sits in a code object of its own (no kernels), which the
+ * runtime loads on a GPU at the first no-alloc call there (the call takes
+ * the array's address), so processes that never call this entry point do
+ * not hold it; once loaded it is held until the process ends. The first
+ * call on a GPU is therefore the one to make outside graph capture or a
+ * loop that must not allocate. A call whose pto_ns5_workspace_bytes exceeds
  * 256 MiB fails before any launch (bf16 up to one 4096x11008 matrix, fp32
  * up to 2048x8192). The call itself allocates nothing: no hipMalloc, no
  * events (kernel timing is off for it). Every call on a GPU shares that

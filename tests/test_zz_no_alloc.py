@@ -2,7 +2,14 @@
 on the same inputs: bit-identical outputs on two calls in a row, the second
 smaller (the shared static scratch keeps the first call's contents), a
 call too large for the scratch refused before any launch, and the aliasing
-rule (out may be G itself, not a partial overlap)."""
+rule (out may be G itself, not a partial overlap), and that the scratch
+takes HBM only once a no-alloc call has run, not in every process that runs
+the library's NS5 kernels."""
+
+import json
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -60,3 +67,41 @@ def test_noalloc_in_place_and_partial_overlap(hip):
     src, dst = store[:256 * 384].view(256, 384), store[8:8 + 256 * 384].view(256, 384)
     with pytest.raises(ValueError, match="not overlap"):
         hip.newton_schulz_orthogonalize_into(src, dst, 1, a, b, c, 1e-7)
+
+
+_SCRATCH_CHILD = r"""
+import json, sys
+import torch
+from pytorch_opt import ops
+assert ops.load_native()
+hip = ops._NATIVE
+a, b, c = 3.4445, -4.7750, 2.0315
+G = (1e-3 * torch.randn(256, 384, device="cuda")).bfloat16()
+out = torch.empty_like(G)
+free = [torch.cuda.mem_get_info()[0]]
+want = hip.newton_schulz_orthogonalize(G, 5, a, b, c, 1e-7)  # NS5 kernels loaded and run
+torch.cuda.synchronize()
+free.append(torch.cuda.mem_get_info()[0])
+hip.newton_schulz_orthogonalize_into(G, out, 5, a, b, c, 1e-7)  # first no-alloc call
+torch.cuda.synchronize()
+free.append(torch.cuda.mem_get_info()[0])
+print(json.dumps({"free": free, "equal": bool(torch.equal(out, want))}))
+"""
+
+
+def test_scratch_held_only_after_a_noalloc_call():
+    """In a fresh process: running pto_ns5 leaves the 256 MiB scratch
+    unallocated; the first no-alloc call is what takes it (its code object
+    is loaded on first use of the array's address)."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ)
+    env["PYTHONPATH"] = os.pathsep.join([os.path.join(root, "pytorch-opt_amd"), env.get("PYTHONPATH", "")])
+    r = subprocess.run([sys.executable, "-c", _SCRATCH_CHILD], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    f0, f1, f2 = res["free"]
+    mib = 1 << 20
+    assert res["equal"]
+    assert f0 - f1 < 128 * mib, (f0 - f1) / mib  # NS5 ran: no scratch yet
+    assert f1 - f2 >= 256 * mib, (f1 - f2) / mib  # the no-alloc call brought it in
