@@ -2,7 +2,8 @@
 on the same inputs: bit-identical outputs on two calls in a row, the second
 smaller (the shared static scratch keeps the first call's contents), a
 call too large for the scratch refused before any launch, and the aliasing
-rule (out may be G itself, not a partial overlap), and that the scratch
+rule (out may be G itself, not a partial overlap), replays of a graph that
+captured it, and that the scratch
 takes HBM only once a no-alloc call has run, not in every process that runs
 the library's NS5 kernels."""
 
@@ -67,6 +68,40 @@ def test_noalloc_in_place_and_partial_overlap(hip):
     src, dst = store[:256 * 384].view(256, 384), store[8:8 + 256 * 384].view(256, 384)
     with pytest.raises(ValueError, match="not overlap"):
         hip.newton_schulz_orthogonalize_into(src, dst, 1, a, b, c, 1e-7)
+
+
+def test_noalloc_replays_in_a_graph(hip):
+    """Captured once in a graph (after a first eager call, which takes the
+    scratch's address), pto_ns5_noalloc replays to the eager result every
+    time, with other no-alloc calls through the same scratch between the
+    replays, and follows new input values written into G."""
+    a, b, c = COEFFS
+    G = _input((2, 512, 768), torch.bfloat16, 11)
+    out = torch.empty_like(G)
+    hip.newton_schulz_orthogonalize_into(G, out, 5, a, b, c, 1e-7)
+    torch.cuda.synchronize()
+    want = hip.newton_schulz_orthogonalize(G, 5, a, b, c, 1e-7)
+    assert torch.equal(out, want)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hip.newton_schulz_orthogonalize_into(G, out, 5, a, b, c, 1e-7)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), i
+        other = _input((384, 1000), torch.bfloat16, 20 + i)
+        o2 = torch.empty_like(other)
+        hip.newton_schulz_orthogonalize_into(other, o2, 5, a, b, c, 1e-7)
+        torch.cuda.synchronize()
+        assert torch.equal(o2, hip.newton_schulz_orthogonalize(other, 5, a, b, c, 1e-7)), i
+    G.copy_(_input((2, 512, 768), torch.bfloat16, 12))
+    want = hip.newton_schulz_orthogonalize(G, 5, a, b, c, 1e-7)
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
 
 
 _SCRATCH_CHILD = r"""
