@@ -158,7 +158,7 @@ constexpr int kErrSub = 64;
 // Epilogue of Mk' = Mi^p·Mk (upper tiles + mirror): writes Mk' and the next
 // Mi and folds max|Mk' − I| into err[b * err_stride + sub] (bitwise max of
 // non-negative values, which keeps NaN; err_stride 0 = one batch maximum;
-// sub spreads the waves over kErrSub words).
+// sub spreads the workgroups over kErrSub words).
 template <typename R>
 struct EpiMk {
   typedef R S;
@@ -204,13 +204,24 @@ struct EpiMk {
   __device__ __forceinline__ void put_t(int b, int j, int i0, const R* v, int n, const PreT&) {
     run(b, j, i0, v, 0, n);
   }
+  // Every thread of the workgroup calls this once at the end of the
+  // kernel: wave maxima, then one atomic per workgroup (one per wave
+  // queued ~33 deep on each word at n = 1024).
   __device__ __forceinline__ void finish(int b) {
+    typedef typename Bits<R>::U U;
     for (int off = 32; off > 0; off >>= 1) {
-      typename Bits<R>::U o = __shfl_xor(mx, off, 64);
+      U o = __shfl_xor(mx, off, 64);
       mx = o > mx ? o : mx;
     }
-    const int sub = (int)((blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) & (kErrSub - 1));
-    if ((threadIdx.x & 63) == 0) atomicMax(err + (int64_t)b * err_stride + sub, mx);
+    __shared__ U wmax[16];
+    const int nw = (int)(blockDim.x >> 6);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      U m = wmax[0];
+      for (int w = 1; w < nw; ++w) m = wmax[w] > m ? wmax[w] : m;
+      atomicMax(err + (int64_t)b * err_stride + (blockIdx.x & (kErrSub - 1)), m);
+    }
   }
 };
 
