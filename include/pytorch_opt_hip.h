@@ -50,7 +50,9 @@ int pto_runtime_version(void);
  * called at pytorch_opt/ops/__init__.py:70; semantics of
  * pytorch_opt/ops/reference.py:71-97 and csrc/pytorch_opt_ops.cpp:65-81.
  * G and out are [batch, rows, cols] of `dtype`. bf16 computes with bf16
- * operands and fp32 accumulation; f32/f64 stay in their own precision.
+ * operands and fp32 accumulation when min(rows, cols) >= 128 (below that
+ * the fp32 chain runs and the result is rounded once, as the reference
+ * computes every bf16 input); f32/f64 stay in their own precision.
  * out may be G itself (in place) but must not otherwise overlap it. G may
  * sit at any element alignment (a G that is not 16-byte aligned is copied
  * into the workspace first).

@@ -34,7 +34,7 @@ def _relfro(got, want):
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-300))
 
 
-@pytest.mark.parametrize("seed", [0, 1])
+@pytest.mark.parametrize("seed", [0, 1, 2, 36, 37])
 def test_ns5_random_shapes(native_backend, seed):
     rng = random.Random(seed)
     for _ in range(12):
@@ -54,7 +54,10 @@ def test_ns5_random_shapes(native_backend, seed):
         work = np.float64 if dtype == torch.float64 else np.float32
         want = oo.ns5(_np(Gd).astype(work), steps=steps)
         tol = {torch.float64: 1e-9, torch.float32: 2e-4, torch.bfloat16: 2e-2}[dtype]
-        assert _relfro(_np(got), want) < tol, case
+        if dtype == torch.bfloat16 and min(m, n) < 128:
+            tol = 5e-3  # the fp32 chain, rounded once
+        err = _relfro(_np(got), want)
+        assert err < tol, (case, err)
 
 
 @pytest.mark.parametrize("seed", [0, 1])
