@@ -52,7 +52,7 @@ def test_linear_factors_are_outer_product_sums(device):
 
 @pytest.mark.parametrize("decay", [0.8, None])
 def test_three_batch_blend(device, decay):
-    gen = torch.Generator().manual_seed(12)
+    gen = torch.Generator().manual_seed(47)
     lin = nn.Linear(4, 2, bias=False).to(device)
     tr = KronTracker(lin, ema_decay=decay)
     batches = [torch.randn(6, 4, generator=gen).to(device) for _ in range(3)]
