@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "pto_common.h"
+#include "upper_order.h"
 
 namespace pto {
 
@@ -151,11 +152,13 @@ __device__ __forceinline__ int xcd_remap(int w, int total, int cus) {
 // Map the linear tile id to (tile_row, tile_col).
 // UPPER, BLOCKED: the upper tiles in blocks of 4 tile rows x 8 tile columns
 // (blocks row-major, tiles row-major inside a block), so the ~32 tiles an XCD
-// runs at once read ~12 operand panels instead of the ~16-22 that whole
-// upper-triangle rows need; measured on the bf16 K-FAC Gram (16384x4096,
-// one round of 253 tiles of 192²): -1 to -3.5% over three A/B calls, the
-// NS5 products unchanged within noise. The small fp32 root tiles run slower
-// with it (n = 1024 +6%) and keep plain rows.
+// runs at once read fewer operand panels than whole upper-triangle rows
+// (14-18 against 16-22 at 22 x 22 tiles); measured on the bf16 K-FAC Gram
+// (16384x4096, one round of 253 tiles of 192²): -1 to -3.5% over three A/B
+// calls. The small fp32 root tiles run slower with it (n = 1024 +6%) and
+// keep plain rows. One-round launches of one matrix with at most 22 x 22
+// tiles use the searched orders of upper_order.h instead (10-11 panels per
+// XCD at 22 x 22).
 template <bool UPPER, bool BLOCKED = false>
 __device__ __forceinline__ void decode_tile(int t, int tiles_m, int tiles_n, int& ti, int& tj) {
   if (UPPER && BLOCKED) {
@@ -369,7 +372,16 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const int b = logical / ntile;
   if (g.guard != nullptr && g.guard[(int64_t)b * g.guard_stride] != 0) return;
   int ti, tj;
-  decode_tile<UPPER, sizeof(T) == 2>(logical - b * ntile, g.tiles_m, g.tiles_n, ti, tj);
+  if (UPPER && gridDim.y == 1 && g.tiles_n <= kUpperOrderMaxT && ntile == g.tiles_n * (g.tiles_n + 1) / 2 &&
+      ntile <= g.cus) {
+    // one round of one matrix: each XCD's contiguous range of logical ids
+    // is a set of upper tiles chosen to read few operand panels
+    const int e = kUpperOrder[kUpperOrderOff[g.tiles_n - 1] + logical];
+    ti = e >> 5;
+    tj = e & 31;
+  } else {
+    decode_tile<UPPER, sizeof(T) == 2>(logical - b * ntile, g.tiles_m, g.tiles_n, ti, tj);
+  }
   const int row0 = ti * BM, col0 = tj * BN;
   // On a diagonal tile of a symmetric product a wave whose sub-tile lies
   // entirely below the diagonal stores nothing (both epilogue passes use

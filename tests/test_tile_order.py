@@ -113,3 +113,50 @@ def test_blocked_upper_order_reads_fewer_panels():
     blocked = panels([_decode_blocked(t, n) for t in range(n * (n + 1) // 2)])
     plain = panels([(i, j) for i in range(n) for j in range(i, n)])
     assert max(blocked) < max(plain) and sum(blocked) < sum(plain)
+
+
+def _upper_order_table():
+    """kUpperOrderOff / kUpperOrder of pytorch-opt_amd/csrc/upper_order.h."""
+    import os
+    import re
+
+    path = os.path.join(os.path.dirname(__file__), "..", "pytorch-opt_amd", "csrc", "upper_order.h")
+    text = open(path).read()
+    tmax = int(re.search(r"kUpperOrderMaxT = (\d+);", text).group(1))
+    off = [int(v) for v in re.search(r"kUpperOrderOff\[\d+\] = \{([^}]*)\}", text).group(1).split(",")]
+    flat = [int(v) for v in re.search(r"kUpperOrder\[\d+\] = \{([^}]*)\}", text).group(1).split(",")]
+    return tmax, off, flat
+
+
+def _xcd_chunks(seq):
+    """The logical ids XCD x runs in a launch of len(seq) < C tiles: one
+    contiguous range per XCD, of the sizes _range gives."""
+    by_xcd = {}
+    for w in range(len(seq)):
+        by_xcd.setdefault(w % XCDS, []).append(seq[_range(w, len(seq))])
+    return list(by_xcd.values())
+
+
+def _chunk_panels(chunks):
+    return [len({i for i, _ in c} | {j for _, j in c}) for c in chunks]
+
+
+def test_one_round_upper_order_table():
+    """For every tile-grid side T the table lists each upper tile (i <= j < T)
+    once, in T(T+1)/2 entries, at the offset the kernel reads; every XCD's
+    share of a one-round launch reads no more operand panels than under the
+    blocked order, and at T = 22 (the 4096² products on 192² tiles) at most
+    11 against the blocked order's 18."""
+    tmax, off, flat = _upper_order_table()
+    assert tmax == 22 and len(off) == tmax
+    for T in range(1, tmax + 1):
+        n = T * (T + 1) // 2
+        assert off[T - 1] == sum(t * (t + 1) // 2 for t in range(1, T))
+        seq = [(e >> 5, e & 31) for e in flat[off[T - 1]:off[T - 1] + n]]
+        assert sorted(seq) == [(i, j) for i in range(T) for j in range(i, T)], T
+        table = _chunk_panels(_xcd_chunks(seq))
+        blocked = _chunk_panels(_xcd_chunks([_decode_blocked(t, T) for t in range(n)]))
+        assert max(table) <= max(blocked), (T, table, blocked)
+        if T == 22:
+            assert max(table) <= 11 and max(blocked) == 18
+    assert len(flat) == off[-1] + tmax * (tmax + 1) // 2
