@@ -98,6 +98,36 @@ def timed(fn, reps=1):
     return sorted(ts)[len(ts) // 2]
 
 
+def warm_gpu(torch, fn, min_s=0.06):
+    """Run fn back to back for at least min_s seconds. After any pause the
+    device clocks take ~20-30 ms of work to leave their idle state (one 4096²
+    NS5 measured 1.21-1.32 ms in its first 20 calls, then 1.175-1.18 ms
+    sustained over the next second), so short timings start from here."""
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= min_s:
+            return
+
+
+def gpu_ms_per_call(torch, fn, min_s=0.05, min_reps=5):
+    """Milliseconds per call of fn on the current stream, after warm_gpu:
+    enough back-to-back calls to fill about min_s seconds, timed by events."""
+    warm_gpu(torch, fn)
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    reps = max(min_reps, int(min_s / max(time.perf_counter() - t0, 1e-6)))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
 # ------------------------------------------------------------ headline (config 2)
 
 def make_ns5_inputs(torch, batch, rows, cols, seed0, dev):
@@ -150,16 +180,13 @@ def bench_factors(torch, ops, hip, dev, cpu):
          "fp32", ("kron_left", "kron_right")),
         ("kfac_gram_bf16_16384x4096", lambda: ops.gram_update_(F, A, beta=0.95, alpha=0.05 / 16384),
          4096 * 4097 * 16384, "bf16", ("gram_update", "gram_update_direct"))]:
-        fn()
-        torch.cuda.synchronize()
+        wall = gpu_ms_per_call(torch, fn) / 1e3  # uninstrumented
         hip.prof_reset()
         hip.prof_enable(True)
         reps = 10
-        t0 = time.perf_counter()
         for _ in range(reps):
             fn()
         torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) / reps
         hip.prof_enable(False)
         kms = sum(hip.prof_query(k)[0] for k in kinds) / reps
         res[name] = {"ms": round(wall * 1e3, 3), "kernel_ms": round(kms, 3),
@@ -194,8 +221,7 @@ def bench_roots(torch, hip, dev, cpu):
         g5 = torch.Generator().manual_seed(5)
         lam = 10 ** (-6 * torch.rand(n, generator=g5, dtype=torch.float64))
         A = ((Q * lam) @ Q.T).float().to(dev)
-        hip.inverse_matrix_root_iters(A, 4, 1e-6, "newton", False, 100, 1e-10)
-        torch.cuda.synchronize()
+        warm_gpu(torch, lambda: hip.inverse_matrix_root_iters(A, 4, 1e-6, "newton", False, 100, 1e-10))
         t0 = time.perf_counter()
         X, iters = hip.inverse_matrix_root_iters(A, 4, 1e-6, "newton", False, 100, 1e-10)
         torch.cuda.synchronize()
@@ -648,16 +674,7 @@ def main():
     achieved = kinds[dom]["tflops"]
 
     single = inputs[0][:1].contiguous()
-    for _ in range(3):
-        ops.newton_schulz_orthogonalize(single)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(10):
-        ops.newton_schulz_orthogonalize(single)
-    e1.record()
-    torch.cuda.synchronize()
-    single_ms = e0.elapsed_time(e1) / 10
+    single_ms = gpu_ms_per_call(torch, lambda: ops.newton_schulz_orthogonalize(single))
     single_tflops = ns5_flops(4096, 4096) / (single_ms / 1e3) / 1e12
 
     cpu_line = cpu_baseline_ns5(torch, inputs, cpu) if cpu else None
