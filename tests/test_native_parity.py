@@ -269,6 +269,7 @@ def test_kron_nonsymmetric_prior_and_fp64(native_backend, m, n):
 @pytest.mark.parametrize("dtype,k,m,n,beta2", [
     (torch.float32, 5, 200, 300, 0.95),     # ragged: G padded, small tiles
     (torch.float32, 48, 2048, 2048, 0.999),  # Shampoo's config-5 attention factors
+    (torch.float32, 2, 4096, 4096, 0.95),   # single calls: one round of 192² tiles in the searched order
     (torch.float32, 70, 96, 64, 1.0),       # two launches (64 per call), plain sums
     (torch.float64, 6, 130, 257, 0.9),
 ])
