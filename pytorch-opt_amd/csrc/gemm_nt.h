@@ -26,6 +26,7 @@
 
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "pto_common.h"
 #include "upper_order.h"
@@ -312,6 +313,16 @@ struct LdsPlan {
   static constexpr int ARR = ((STAGE > EPI ? STAGE : EPI) + 15) / 16 * 16;
 };
 
+// An epilogue functor may carry a skip hook, `bool skip(int b, bool first)
+// const`, evaluated by every wave of every workgroup before any other work:
+// true skips matrix b (the workgroup exits). It must return the same value
+// in every wave of a workgroup; `first` marks one workgroup per matrix (the
+// first tile of b), which may record the decision for later launches.
+template <class E, class = void>
+struct HasSkip : std::false_type {};
+template <class E>
+struct HasSkip<E, std::void_t<decltype(std::declval<const E&>().skip(0, false))>> : std::true_type {};
+
 // PT: P is stored [K][M] (M contiguous) and read like a QN operand. For a
 // symmetric P (B' in X' = B'·X, A in A·A) that is P itself: its rows are
 // its columns, so the product reads it with conflict-free transposing LDS
@@ -371,6 +382,9 @@ __global__ void __launch_bounds__(Cfg::NT) gemm_nt_kernel(GemmArgs g, Epi epi) {
   const int logical = xcd_remap(blockIdx.y * ntile + blockIdx.x, ntile * gridDim.y, g.cus);
   const int b = logical / ntile;
   if (g.guard != nullptr && g.guard[(int64_t)b * g.guard_stride] != 0) return;
+  if constexpr (HasSkip<Epi>::value) {
+    if (epi.skip(b, logical == b * ntile)) return;
+  }
   int ti, tj;
   if (UPPER && gridDim.y == 1 && g.tiles_n <= kUpperOrderMaxT && ntile == g.tiles_n * (g.tiles_n + 1) / 2 &&
       ntile <= g.cus) {

@@ -31,11 +31,15 @@
 // residual of the blocked sums).
 //
 // Device-side control: every kernel of an iteration checks a device flag
-// and exits at once after the stop decision, and a one-thread kernel makes
-// that decision from err. The host enqueues iterations in chunks and reads
-// the flag once per chunk instead of once per iteration. X ping-pongs
-// between two buffers, so the "previous iterate" is still intact when the
-// divergence guard fires.
+// and exits at once after the stop decision. The decision for iteration it
+// is made by every wave of iteration it + 1's first launch (from the state
+// after it - 1 and err of it; its first workgroup records the new state),
+// so no launch sits between iterations; states alternate between two slots
+// by iteration parity, so a launch never reads the slot it writes. The host
+// enqueues iterations in chunks, ends each chunk with a one-block decide
+// kernel, and reads the state once per chunk instead of once per
+// iteration. X ping-pongs between two buffers, so the "previous iterate"
+// is still intact when the divergence guard fires.
 #include <algorithm>
 #include <limits>
 #include <vector>
@@ -252,13 +256,20 @@ __device__ R err_slot_max(const R* slot) {
   return r;
 }
 
-// Global mode: one thread applies the rule to slot it. Per-matrix mode: the
-// block applies it to each matrix (slot it·nb + b) and then to the summary.
+// States after iteration it (`out`) from those after it - 1 (`in`) and
+// err of it. Global mode: one thread applies the rule to slot it.
+// Per-matrix mode: the block applies it to each matrix (slot it·nb + b)
+// and then to the summary (only these chunk-end launches refresh the
+// summary; its stop flag is all the host reads of it).
 template <typename R>
-__global__ void __launch_bounds__(256) root_decide_kernel(RootState<R>* st, const R* __restrict__ err, int it, R tol,
-                                                          int nb, int each) {
+__global__ void __launch_bounds__(256) root_decide_kernel(const RootState<R>* in, RootState<R>* out,
+                                                          const R* __restrict__ err, int it, R tol, int nb, int each) {
   if (!each) {
-    if (threadIdx.x == 0) decide_one(st[0], err_slot_max(err + (int64_t)it * kErrSub), it, tol);
+    if (threadIdx.x == 0) {
+      RootState<R> d = in[0];
+      decide_one(d, err_slot_max(err + (int64_t)it * kErrSub), it, tol);
+      out[0] = d;
+    }
     return;
   }
   __shared__ int live;
@@ -266,16 +277,59 @@ __global__ void __launch_bounds__(256) root_decide_kernel(RootState<R>* st, cons
   __syncthreads();
   int mine = 0;
   for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-    decide_one(st[1 + b], err_slot_max(err + ((int64_t)it * nb + b) * kErrSub), it, tol);
-    mine |= !st[1 + b].stopped;
+    RootState<R> d = in[1 + b];
+    decide_one(d, err_slot_max(err + ((int64_t)it * nb + b) * kErrSub), it, tol);
+    out[1 + b] = d;
+    mine |= !d.stopped;
   }
   if (mine) atomicOr(&live, 1);
   __syncthreads();
-  if (threadIdx.x == 0 && !st[0].stopped) {
-    st[0].iters = it + 1;
-    if (!live) st[0].stopped = 1;
+  if (threadIdx.x == 0) {
+    RootState<R> d = in[0];
+    if (!d.stopped) {
+      d.iters = it + 1;
+      if (!live) d.stopped = 1;
+    }
+    out[0] = d;
   }
 }
+
+// Store epilogue of iteration it + 1's first launch (X·Mi, paired with
+// Mi·Mi for one matrix) that makes the stop decision of iteration `it`
+// itself: every wave reduces the kErrSub error words (one per lane) and
+// applies the rule to the state after it - 1, all waves alike; the first
+// workgroup of each run records the state after `it` for the later
+// launches. A stopped run skips the product.
+template <typename R>
+struct EpiStoreDecide : EpiStore<R, R> {
+  const RootState<R>* prev;  // states after iteration it - 1
+  RootState<R>* next;        // states after iteration it (written here)
+  const R* err;              // error words of iteration it
+  int it;
+  R tol;
+  int state0;      // state index of run 0 (1 in per-matrix mode, else 0)
+  int per_matrix;  // batch entry b is run b (own state and error words);
+                   // else every entry belongs to run 0 (one batch-wide
+                   // rule, or the X·Mi / Mi·Mi pair of one matrix)
+  __device__ __forceinline__ bool skip(int b, bool first) const {
+    typedef typename Bits<R>::U U;
+    static_assert(kErrSub == 64, "one error word per lane");
+    const int r = per_matrix ? b : 0;
+    const int s = state0 + r;
+    const U* w = reinterpret_cast<const U*>(err + (int64_t)r * kErrSub);
+    U m = w[threadIdx.x & (kErrSub - 1)];
+    for (int off = 32; off > 0; off >>= 1) {
+      const U o = __shfl_xor(m, off, 64);
+      m = o > m ? o : m;
+    }
+    R e;
+    __builtin_memcpy(&e, &m, sizeof(R));
+    RootState<R> d = prev[s];
+    decide_one(d, e, it, tol);
+    if (first && b == r && threadIdx.x == 0) next[s] = d;
+    return d.stopped != 0;
+  }
+};
 
 // out = sym(X_result) cast to the input dtype.
 template <typename R, typename TO>
@@ -314,7 +368,7 @@ size_t root_ws_bytes_t(int64_t batch, int64_t n, int64_t max_iter, bool each) {
   add(sizeof(R) * batch);
   add(sizeof(R) * batch);
   add(sizeof(R) * std::max<int64_t>(max_iter, 1) * (each ? batch : 1) * kErrSub);
-  add(sizeof(RootState<R>) * (each ? 1 + batch : 1));
+  add(sizeof(RootState<R>) * 2 * (each ? 1 + batch : 1));
   for (int i = 0; i < kRootBufs; ++i) add(sizeof(R) * batch * n * ld);
   return bytes + 256;
 }
@@ -339,7 +393,7 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   const int64_t n_err = std::max<int64_t>(max_iter, 1) * (each ? batch : 1) * kErrSub;
   const int64_t n_st = each ? 1 + batch : 1;
   R* err = cv.take<R>(n_err);
-  RootState<R>* st = cv.take<RootState<R>>(n_st);
+  RootState<R>* st = cv.take<RootState<R>>(2 * n_st);  // two slots of n_st
   R* buf[kRootBufs];
   for (int i = 0; i < kRootBufs; ++i) buf[i] = cv.take<R>(batch * sb);
   PTO_REQUIRE(!cv.overflow, "inverse_matrix_root: workspace too small");
@@ -371,11 +425,15 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   for (R* q : {X[1], Mi[1], Mk[1], tmp[0], tmp[1], tmp[2]})
     if (launch_zero_cols<R>(q, n, ld, n, sb, nb, stream)) return -1;
   if (launch_fill<R>(err, n_err, R(0), stream)) return -1;
-  if (launch_fill<int>(reinterpret_cast<int*>(st), n_st * (int64_t)(sizeof(RootState<R>) / sizeof(int)), 0, stream))
+  if (launch_fill<int>(reinterpret_cast<int*>(st), 2 * n_st * (int64_t)(sizeof(RootState<R>) / sizeof(int)), 0,
+                      stream))
     return -1;
+  // states after iteration i (slot of i = -1: the zeroed initial state)
+  auto slot = [&](int64_t i) -> RootState<R>* { return st + (i & 1) * n_st; };
 
-  // GEMMs skip a stopped run: the one state, or matrix b's own
-  const int* guard = each ? &st[1].stopped : &st[0].stopped;
+  // GEMMs skip a stopped run: the one state, or matrix b's own (set per
+  // iteration to the states after the previous one)
+  const int* guard = nullptr;
   const int guard_stride = each ? (int)(sizeof(RootState<R>) / sizeof(int)) : 0;
   // dst = P·Q for symmetric Q (Q's rows are its columns); upper = the
   // product is symmetric too, computed on upper tiles and mirrored.
@@ -392,19 +450,39 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
   // one-matrix launch that would leave CUs idle; each product's arithmetic
   // is unchanged).
   const bool pair = nb == 1 && p >= 2;
-  auto product_pair = [&](const R* P0, R* d0, const R* P1, R* d1, const R* Q, const char* name) -> int {
+  // The first launch of iteration it >= 1 decides iteration it - 1 itself.
+  auto decider = [&](int it, R* dst, int64_t sd, bool per_matrix) {
+    return EpiStoreDecide<R>{{dst, ld, sd, vec_ok<R>(dst, ld, sd)},
+                             slot(it - 2),
+                             slot(it - 1),
+                             err + (int64_t)(it - 1) * (each ? nb : 1) * kErrSub,
+                             it - 1,
+                             static_cast<R>(tol),
+                             each ? 1 : 0,
+                             per_matrix ? 1 : 0};
+  };
+  auto product_pair = [&](int it, const R* P0, R* d0, const R* P1, R* d1, const R* Q, const char* name) -> int {
     GemmArgs g{P0, ld, (int64_t)(P1 - P0), Q, ld, 0, (int)n, (int)n, (int)ld, 0, 0, guard, 0};
     const int64_t sd = (int64_t)(d1 - d0);
+    if (it > 0) {
+      g.guard = nullptr;
+      return launch_gemm<R, true, EpiStoreDecide<R>, true>(g, decider(it, d0, sd, false), 2, stream, name);
+    }
     EpiStore<R, R> e{d0, ld, sd, vec_ok<R>(d0, ld, sd)};
     return launch_gemm<R, true, EpiStore<R, R>, true>(g, e, 2, stream, name);
   };
 
   auto iteration = [&](int it) -> int {
     const int cur = it & 1, nxt = cur ^ 1;
+    guard = &slot(it - 1)[each ? 1 : 0].stopped;
     // X_{it+1} = X_it · Mi (symmetric: both are polynomials in M); with
     // `pair`, tmp[0] = Mi·Mi in the same launch
     if (pair) {
-      if (product_pair(X[cur], X[nxt], Mi[cur], tmp[0], Mi[cur], "root_xmi_pow")) return -1;
+      if (product_pair(it, X[cur], X[nxt], Mi[cur], tmp[0], Mi[cur], "root_xmi_pow")) return -1;
+    } else if (it > 0) {
+      GemmArgs g{X[cur], ld, sb, Mi[cur], ld, sb, (int)n, (int)n, (int)ld, 0, 0, nullptr, 0};
+      if (launch_gemm<R, true, EpiStoreDecide<R>, true>(g, decider(it, X[nxt], sb, each), nb, stream, "root_xmi"))
+        return -1;
     } else if (product(X[cur], Mi[cur], X[nxt], true, "root_xmi")) {
       return -1;
     }
@@ -463,9 +541,6 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
                  reinterpret_cast<U*>(err + (int64_t)it * (each ? nb : 1) * kErrSub), each ? kErrSub : 0, U(0), vec_ok<R>(Mk[nxt], ld, sb) && vec_ok<R>(Mi[nxt], ld, sb)};
       if (launch_gemm<R, true, EpiMk<R>, true>(g, e, nb, stream, "root_mk")) return -1;
     }
-    hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(each ? 256 : 64), 0, stream, st, err, it,
-                       static_cast<R>(tol), nb, (int)each);
-    PTO_LAUNCHED("root_decide");
     return 0;
   };
 
@@ -476,21 +551,25 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     const int64_t end = std::min<int64_t>(max_iter, it + chunk);
     for (; it < end; ++it)
       if (iteration((int)it)) return -1;
-    PTO_HIP(hipMemcpyAsync(&host, st, sizeof(host), hipMemcpyDeviceToHost, stream));
+    hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(each ? 256 : 64), 0, stream, slot(it - 2),
+                       slot(it - 1), err, (int)(it - 1), static_cast<R>(tol), nb, (int)each);
+    PTO_LAUNCHED("root_decide");
+    PTO_HIP(hipMemcpyAsync(&host, slot(it - 1), sizeof(host), hipMemcpyDeviceToHost, stream));
     PTO_HIP(hipStreamSynchronize(stream));
     if (host.stopped) break;
     chunk = std::min<int64_t>(chunk * 2, 16);
   }
+  const RootState<R>* last = slot(it - 1);  // states after the last iteration run
   {
     dim3 grid((unsigned)((n + 31) / 32), (unsigned)((n + 31) / 32), (unsigned)nb);
-    hipLaunchKernelGGL((root_final_kernel<R, TI>), grid, dim3(256), 0, stream, X[0], X[1], st, (int)each, n, ld, sb,
-                       out);
+    hipLaunchKernelGGL((root_final_kernel<R, TI>), grid, dim3(256), 0, stream, X[0], X[1], last, (int)each, n, ld,
+                       sb, out);
     PTO_LAUNCHED("root_final");
   }
   if (iters_out && !each) *iters_out = host.iters;
   if (iters_out && each) {
     std::vector<RootState<R>> all((size_t)nb);
-    PTO_HIP(hipMemcpyAsync(all.data(), st + 1, sizeof(RootState<R>) * nb, hipMemcpyDeviceToHost, stream));
+    PTO_HIP(hipMemcpyAsync(all.data(), last + 1, sizeof(RootState<R>) * nb, hipMemcpyDeviceToHost, stream));
     PTO_HIP(hipStreamSynchronize(stream));
     for (int b = 0; b < nb; ++b) iters_out[b] = all[b].iters;
   }

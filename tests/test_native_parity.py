@@ -556,6 +556,32 @@ def test_root_divergence_guard_and_max_iter(native_backend):
         assert it_k == k and np.abs(_np(got_k) - want_k).max() < 1e-12
 
 
+@pytest.mark.parametrize("max_iter", [2, 5, 6, 7, 13, 14, 15])
+def test_root_stop_rule_across_chunk_ends(native_backend, max_iter):
+    """The host reads the stop state after iterations 1, 5, 13, 29, ...;
+    in between, each iteration's first launch applies the rule of the one
+    before. Runs cut by max_iter on either side of those ends, and runs whose
+    tol (or divergence guard) stops them inside a chunk, return the oracle's
+    iterate and iteration count (fp64)."""
+    S = _spd_spread(13, 305).double()
+    for tol in (1e-10, 1e-3):
+        want, it_o = oo.inverse_root(S.numpy(), 4, method="newton", max_iter=max_iter, tol=tol)
+        got, it_h = native_backend.inverse_matrix_root_iters(S.to(DEV), 4, 0.0, "newton", True, max_iter, tol)
+        assert it_h == it_o, (max_iter, tol, it_h, it_o)
+        assert np.abs(_np(got) - want).max() < 1e-12 * max(1.0, np.abs(want).max())
+    # one small negative eigenvalue: the guard fires after 5, 6 or 8
+    # iterations (sooner the more negative it is)
+    rng = np.random.default_rng(5)
+    Q, _ = np.linalg.qr(rng.standard_normal((12, 12)))
+    for neg in (-0.03, -0.01, -0.003):
+        A = (Q * np.concatenate([np.linspace(1, 2, 11), [neg]])) @ Q.T
+        want, it_o = oo.inverse_root(A, 2, method="newton", max_iter=max_iter, root_dtype=np.float64)
+        got, it_h = native_backend.inverse_matrix_root_iters(torch.from_numpy(A).to(DEV), 2, 0.0, "newton", True,
+                                                             max_iter, 1e-10)
+        assert it_h == it_o, (max_iter, neg, it_h, it_o)
+        assert np.abs(_np(got) - want).max() < 1e-9 * max(1.0, np.abs(want).max())
+
+
 @pytest.mark.parametrize("root_f64", [True, False])
 def test_root_each_matches_separate_calls(native_backend, root_f64):
     """Per-matrix stop mode: a stack holding a well-conditioned SPD matrix,
