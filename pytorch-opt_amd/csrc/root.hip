@@ -38,7 +38,8 @@
 // by iteration parity, so a launch never reads the slot it writes. The host
 // enqueues iterations in chunks, ends each chunk with a one-block decide
 // kernel, and reads the state once per chunk instead of once per
-// iteration. X ping-pongs between two buffers, so the "previous iterate"
+// iteration, one chunk behind the enqueued work (a chunk enqueued past the
+// stop only runs skipping launches). X ping-pongs between two buffers, so the "previous iterate"
 // is still intact when the divergence guard fires.
 #include <algorithm>
 #include <limits>
@@ -358,6 +359,22 @@ __global__ void __launch_bounds__(256) root_final_kernel(const R* __restrict__ X
 
 constexpr int kRootBufs = 10;
 
+// Host copies of the stop state after each chunk of iterations, two per
+// host thread, in pinned memory so that the copies are asynchronous and the
+// host can enqueue the next chunk before it waits for this one's state.
+// Allocated on first use and kept until the process ends.
+constexpr size_t kPinSlot = 64;
+static_assert(sizeof(RootState<double>) <= kPinSlot && sizeof(RootState<float>) <= kPinSlot, "state copy slot");
+static char* pinned_states() {
+  static thread_local char* buf = nullptr;
+  if (buf == nullptr) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 2 * kPinSlot, hipHostMallocPortable) != hipSuccess) return nullptr;
+    buf = static_cast<char*>(p);
+  }
+  return buf;
+}
+
 // each: per-matrix stop mode (err slots and states per matrix).
 template <typename R>
 size_t root_ws_bytes_t(int64_t batch, int64_t n, int64_t max_iter, bool each) {
@@ -544,20 +561,51 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     return 0;
   };
 
+  struct Events {
+    hipEvent_t e[2] = {nullptr, nullptr};
+    ~Events() {
+      for (hipEvent_t x : e)
+        if (x) (void)hipEventDestroy(x);
+    }
+  } ev;
+  for (hipEvent_t& x : ev.e) PTO_HIP(hipEventCreateWithFlags(&x, hipEventDisableTiming));
+  char* pin = pinned_states();
+  PTO_REQUIRE(pin != nullptr, "inverse_matrix_root: pinned host buffer allocation failed");
+  RootState<R>* hs[2] = {reinterpret_cast<RootState<R>*>(pin), reinterpret_cast<RootState<R>*>(pin + kPinSlot)};
+
   RootState<R> host{};
   int64_t it = 0;
   int64_t chunk = 2;
-  while (it < max_iter) {
+  // Enqueue the next chunk of iterations, the chunk-end decide and the copy
+  // of the state after the chunk into hs[k].
+  auto enqueue_chunk = [&](int k) -> int {
     const int64_t end = std::min<int64_t>(max_iter, it + chunk);
     for (; it < end; ++it)
       if (iteration((int)it)) return -1;
     hipLaunchKernelGGL(root_decide_kernel<R>, dim3(1), dim3(each ? 256 : 64), 0, stream, slot(it - 2),
                        slot(it - 1), err, (int)(it - 1), static_cast<R>(tol), nb, (int)each);
     PTO_LAUNCHED("root_decide");
-    PTO_HIP(hipMemcpyAsync(&host, slot(it - 1), sizeof(host), hipMemcpyDeviceToHost, stream));
-    PTO_HIP(hipStreamSynchronize(stream));
-    if (host.stopped) break;
+    PTO_HIP(hipMemcpyAsync(hs[k], slot(it - 1), sizeof(RootState<R>), hipMemcpyDeviceToHost, stream));
+    PTO_HIP(hipEventRecord(ev.e[k], stream));
     chunk = std::min<int64_t>(chunk * 2, 16);
+    return 0;
+  };
+  if (max_iter > 0) {
+    if (enqueue_chunk(0)) return -1;
+    for (int k = 0;; k ^= 1) {
+      // the next chunk is enqueued before the host waits for this one, so
+      // the device does not idle while the host reads the state
+      const bool ahead = it < max_iter;
+      if (ahead && enqueue_chunk(k ^ 1)) return -1;
+      PTO_HIP(hipEventSynchronize(ev.e[k]));
+      host = *hs[k];
+      if (!ahead || host.stopped) {
+        // a chunk enqueued past a stop only skips (its state is this one);
+        // its copy lands before this thread's buffer can be reused
+        if (ahead) PTO_HIP(hipEventSynchronize(ev.e[k ^ 1]));
+        break;
+      }
+    }
   }
   const RootState<R>* last = slot(it - 1);  // states after the last iteration run
   {
