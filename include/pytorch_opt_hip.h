@@ -212,6 +212,43 @@ int pto_adamw_step(void* p, const void* g, void* m, void* v, int dtype, int64_t 
                    size_t ws_bytes, void* stream);
 
 /*
+ * Muon's elementwise work around NS5, pytorch_opt/optim/muon.py:79-92
+ * (torch elementwise ops in the reference; no compiled counterpart).
+ * pto_muon_momentum: buf <- buf*mu + g (mul_ then add_), then
+ *   u <- g + mu*buf (nesterov != 0; one fused multiply-add, as torch's
+ *   g.add(buf, alpha=mu)) or u <- buf; u is a separate array of n elements
+ *   (the caller's stacked NS5 input), buf and g are updated/read in place.
+ * pto_muon_update: p <- p*decay (skipped when decay == 1), then
+ *   p <- p + neg_lr*o (one fused multiply-add, as p.add_(o, alpha=neg_lr));
+ *   update_sq (device pointer) receives the sum of o^2 in double, summed in
+ *   a fixed order (the update_rms diagnostic, muon.py:92).
+ * Each result is rounded to `dtype` in the reference's op order.
+ */
+size_t pto_muon_update_workspace_bytes(void);
+int pto_muon_momentum(void* buf, const void* g, void* u, int dtype, int64_t n, double momentum, int nesterov,
+                      void* stream);
+int pto_muon_update(void* p, const void* o, int dtype, int64_t n, double decay, double neg_lr, double* update_sq,
+                    void* workspace, size_t ws_bytes, void* stream);
+
+/*
+ * Shampoo's AdaGrad graft and parameter update, pytorch_opt/optim/
+ * shampoo.py:133-151 (torch elementwise ops and two norms in the reference;
+ * no compiled counterpart), over n elements of `dtype`:
+ *   acc <- acc + g*g (addcmul_: g*g rounded, then the sum);
+ *   t <- ||g / (sqrt(acc) + diag_eps)||;
+ *   ratio <- t / (||P|| + 1e-30);  u <- P*ratio;
+ *   momentum != 0: buf <- buf*momentum + u, u <- buf (buf must be non-NULL
+ *   exactly when momentum != 0);
+ *   p <- p*decay (skipped when decay == 1);  p <- p + neg_lr*u.
+ * The norms are fixed-order double sums rounded to `dtype`; ratio_out
+ * (device pointer to one `dtype` element, may be NULL) receives the ratio.
+ */
+size_t pto_shampoo_graft_workspace_bytes(void);
+int pto_shampoo_graft(void* p, const void* g, void* acc, const void* P, void* buf, int dtype, int64_t n,
+                      double diag_eps, double momentum, double decay, double neg_lr, void* ratio_out, void* workspace,
+                      size_t ws_bytes, void* stream);
+
+/*
  * Kernel timing with HIP events. The reference has no counterpart (its
  * StepTimer, pytorch_opt/optim/_common.py:82-98, is host wall-clock). While
  * enabled, every MFMA launch is bracketed by events on its stream;

@@ -144,6 +144,31 @@ def adamw_step_(p, grad, exp_avg, exp_avg_sq, lr, weight_decay, betas, eps, step
                                  return_update_sq=return_update_sq)
 
 
+def muon_momentum_(buf, grad, u, momentum, nesterov=True):
+    """(additive) Muon's momentum step in one pass: buf ← buf·μ + g in place,
+    the NS5 input (g + μ·buf, or buf) into u. Returns u."""
+    if _use_native():
+        return _NATIVE.muon_momentum_(buf, grad, u, float(momentum), bool(nesterov))
+    return reference.muon_momentum_(buf, grad, u, momentum, nesterov)
+
+
+def muon_update_(p, O, decay, neg_lr):
+    """(additive) Muon's parameter update in one pass: p ← p·decay + neg_lr·O
+    (decay applied only when ≠ 1); returns Σ O² as a 0-dim tensor."""
+    if _use_native():
+        return _NATIVE.muon_update_(p, O, float(decay), float(neg_lr))
+    return reference.muon_update_(p, O, decay, neg_lr)
+
+
+def shampoo_graft_(p, grad, acc, P, buf, diag_eps, momentum, decay, neg_lr):
+    """(additive) Shampoo's AdaGrad graft and parameter update in two passes;
+    returns the graft ratio as a 0-dim tensor."""
+    if _use_native():
+        return _NATIVE.shampoo_graft_(p, grad, acc, P, buf, float(diag_eps), float(momentum), float(decay),
+                                      float(neg_lr))
+    return reference.shampoo_graft_(p, grad, acc, P, buf, diag_eps, momentum, decay, neg_lr)
+
+
 def gram_update_(F, X, beta=0.0, alpha=1.0, append_ones=False):
     """F ← beta·F + alpha·X̃ᵀX̃ in place, X̃ = [X, 1] if append_ones (beta=0 overwrites)."""
     if _use_native():
@@ -156,7 +181,8 @@ __all__ = ["get_backend", "set_backend", "native_available", "load_native", "inv
            "inverse_matrix_root_each",
            "newton_schulz_orthogonalize", "kron_factor_update_", "kron_factor_update_batched_",
            "precond_apply_two_sided",
-           "two_sided_product", "gram_update_", "adamw_step_", "OpsArgumentError", "reference"]
+           "two_sided_product", "gram_update_", "adamw_step_", "muon_momentum_", "muon_update_", "shampoo_graft_",
+           "OpsArgumentError", "reference"]
 
 if os.environ.get("PYTORCH_OPT_NATIVE") == "1":
     load_native()

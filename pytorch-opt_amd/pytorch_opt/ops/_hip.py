@@ -69,6 +69,12 @@ SIGNATURES = {
     "pto_adamw_workspace_bytes": (_c_size, []),
     "pto_adamw_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_dbl, _c_dbl, _c_dbl,
                                 _c_dbl, _c_i64, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "pto_muon_update_workspace_bytes": (_c_size, []),
+    "pto_muon_momentum": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_int, _c_ptr]),
+    "pto_muon_update": (_c_int, [_c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_dbl, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "pto_shampoo_graft_workspace_bytes": (_c_size, []),
+    "pto_shampoo_graft": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_dbl, _c_dbl, _c_dbl,
+                                   _c_dbl, _c_ptr, _c_ptr, _c_size, _c_ptr]),
     "pto_prof_enable": (_c_int, [_c_int]),
     "pto_prof_reset": (_c_int, []),
     "pto_prof_query": (_c_int, [ctypes.c_char_p, ctypes.POINTER(_c_dbl), ctypes.POINTER(_c_i64)]),
@@ -382,6 +388,50 @@ class HipBackend:
                                                              nbytes, stream)
                 self._check(rc, what)
         return out.reshape(*lead, m, n)
+
+    @staticmethod
+    def _fusable(*ts) -> bool:
+        """Same device (a GPU), dtype with a kernel, element count, and
+        contiguous: the fused elementwise kernels' preconditions."""
+        t0 = ts[0]
+        return (all(t.is_cuda and t.device == t0.device for t in ts) and t0.dtype in _DTYPE_CODE
+                and all(t.dtype == t0.dtype and t.numel() == t0.numel() and t.is_contiguous() for t in ts))
+
+    def muon_momentum_(self, buf, g, u, momentum, nesterov):
+        if buf.shape != g.shape or not self._fusable(buf, g, u):
+            return reference.muon_momentum_(buf, g, u, momentum, nesterov)
+        with torch.cuda.device(buf.device):
+            rc = self._lib.pto_muon_momentum(_ptr(buf), _ptr(g), _ptr(u), _DTYPE_CODE[buf.dtype], buf.numel(),
+                                             float(momentum), int(bool(nesterov)), self._stream(buf.device))
+        self._check(rc, "muon_momentum_")
+        return u
+
+    def muon_update_(self, p, O, decay, neg_lr):
+        if not self._fusable(p, O):
+            return reference.muon_update_(p, O, decay, neg_lr)
+        sq = torch.empty((), dtype=torch.float64, device=p.device)
+        with torch.cuda.device(p.device):
+            nbytes = self._lib.pto_muon_update_workspace_bytes()
+            ws = self._workspace(nbytes, p.device)
+            rc = self._lib.pto_muon_update(_ptr(p), _ptr(O), _DTYPE_CODE[p.dtype], p.numel(), float(decay),
+                                           float(neg_lr), _ptr(sq), _ptr(ws), nbytes, self._stream(p.device))
+        self._check(rc, "muon_update_")
+        return sq
+
+    def shampoo_graft_(self, p, g, acc, P, buf, diag_eps, momentum, decay, neg_lr):
+        ts = (p, g, acc, P) + ((buf,) if buf is not None else ())
+        if (buf is not None) != bool(momentum) or g.shape != acc.shape or not self._fusable(*ts):
+            return reference.shampoo_graft_(p, g, acc, P, buf, diag_eps, momentum, decay, neg_lr)
+        ratio = torch.empty((), dtype=p.dtype, device=p.device)
+        with torch.cuda.device(p.device):
+            nbytes = self._lib.pto_shampoo_graft_workspace_bytes()
+            ws = self._workspace(nbytes, p.device)
+            rc = self._lib.pto_shampoo_graft(_ptr(p), _ptr(g), _ptr(acc), _ptr(P),
+                                             _ptr(buf) if buf is not None else None, _DTYPE_CODE[p.dtype],
+                                             p.numel(), float(diag_eps), float(momentum), float(decay),
+                                             float(neg_lr), _ptr(ratio), _ptr(ws), nbytes, self._stream(p.device))
+        self._check(rc, "shampoo_graft_")
+        return ratio
 
     def adamw_step_(self, p, g, m, v, lr, weight_decay, beta1, beta2, eps, step, return_update_sq):
         tensors = (p, g, m, v)

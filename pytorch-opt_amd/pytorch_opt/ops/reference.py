@@ -160,6 +160,44 @@ def adamw_step_(p, grad, exp_avg, exp_avg_sq, lr, weight_decay, betas, eps, step
     return update.pow(2).sum() if return_update_sq else None
 
 
+def muon_momentum_(buf, grad, u, momentum, nesterov=True):
+    """Muon's momentum step (optim/muon.py:79-83): buf ← buf·μ + g in place,
+    then the NS5 input g + μ·buf (Nesterov) or buf, written into u (a tensor
+    of buf's size, e.g. one slot of a stacked batch). Returns u."""
+    buf.mul_(momentum).add_(grad)
+    src = grad.add(buf, alpha=momentum) if nesterov else buf
+    u.copy_(src.reshape(u.shape))
+    return u
+
+
+def muon_update_(p, O, decay, neg_lr):
+    """Muon's parameter update (optim/muon.py:87-92): p ← p·decay (when
+    decay ≠ 1), p ← p + neg_lr·O; returns Σ O² (the update_rms term)."""
+    if decay != 1.0:
+        p.mul_(decay)
+    upd = O.reshape(p.shape)
+    p.add_(upd, alpha=neg_lr)
+    return upd.pow(2).sum()
+
+
+def shampoo_graft_(p, grad, acc, P, buf, diag_eps, momentum, decay, neg_lr):
+    """Shampoo's AdaGrad graft and update (optim/shampoo.py:133-151):
+    acc ← acc + g·g; ratio = ‖g/(√acc + diag_eps)‖ / (‖P‖ + 1e-30); u = P·ratio;
+    with momentum buf ← buf·μ + u, u = buf; p ← p·decay (when decay ≠ 1);
+    p ← p + neg_lr·u. Returns the ratio as a 0-dim tensor."""
+    acc.addcmul_(grad, grad)
+    target = (grad / (acc.sqrt() + diag_eps)).norm()
+    ratio = target / (P.norm() + 1e-30)
+    upd = (P * ratio).reshape(p.shape)
+    if momentum:
+        buf.mul_(momentum).add_(upd)
+        upd = buf
+    if decay != 1.0:
+        p.mul_(decay)
+    p.add_(upd, alpha=neg_lr)
+    return ratio
+
+
 def two_sided_product(A, X, B, transpose_a=False, transpose_b=False):
     """op(A)·X·op(B), op = identity or transpose, associated left to right.
 

@@ -13,9 +13,13 @@ and each bucket is orthogonalised by one batched NS5 launch (up to
 ``ns_batch_bytes`` of stacked input per launch). NS5 treats every matrix
 of a batch independently, so the parameters end where the per-parameter
 loop would put them; the batched launch fills the GPU where one 2048²
-matrix cannot. The ``update_rms`` diagnostic is summed in the reference's
-parameter order from per-parameter sums read back with one host
-synchronisation per step instead of one per parameter.
+matrix cannot. The momentum step writes each parameter's NS5 input
+straight into its slot of the stacked batch (``ops.muon_momentum_``, one
+pass) and the update applies decay, step and the Σ update² term in one
+pass (``ops.muon_update_``); the reference's torch ops for both run the
+same arithmetic in five and three passes. The ``update_rms`` diagnostic is
+summed in the reference's parameter order from per-parameter sums read
+back with one host synchronisation per step instead of one per parameter.
 """
 
 from __future__ import annotations
@@ -73,28 +77,29 @@ class Muon(Optimizer, DiagnosticsMixin):
     # parameter on its own, as the reference does.
     ns_batch_bytes = 4 << 30
 
-    def _orthogonalize_bucket(self, group, items, contrib):
-        """NS5 of the bucket's stacked matrices, then each parameter's update."""
+    def _orthogonalize_bucket(self, group, shape2, items, contrib):
+        """Momentum into the stacked NS5 input, NS5, then each parameter's update."""
         limit = self.ns_batch_bytes
+        mu, nesterov = group["momentum"], group["nesterov"]
+        decay = 1.0 - group["lr"] * group["weight_decay"] if group["weight_decay"] else 1.0
         start = 0
         while start < len(items):
             end = start + 1
-            per = items[start][1].numel() * items[start][1].element_size()
+            per = items[start][0].numel() * items[start][0].element_size()
             while end < len(items) and (end - start + 1) * per <= limit:
                 end += 1
             chunk = items[start:end]
+            p0 = chunk[0][0]
+            U = torch.empty((len(chunk),) + shape2, dtype=p0.dtype, device=p0.device)
+            for i, (p, g, buf, _) in enumerate(chunk):
+                ops.muon_momentum_(buf, g, U[i], mu, nesterov)
             if len(chunk) == 1:
-                outs = [ops.newton_schulz_orthogonalize(chunk[0][1], steps=group["ns_steps"])]
+                outs = [ops.newton_schulz_orthogonalize(U[0], steps=group["ns_steps"])]
             else:
-                O = ops.newton_schulz_orthogonalize(torch.stack([u2 for _, u2, _ in chunk]), steps=group["ns_steps"])
-                outs = O.unbind(0)
-            for (p, _, slot), O in zip(chunk, outs):
+                outs = ops.newton_schulz_orthogonalize(U, steps=group["ns_steps"]).unbind(0)
+            for (p, _, _, slot), O in zip(chunk, outs):
                 lr_eff = group["lr"] * self._scale(O.shape, group["lr_adjust"])
-                if group["weight_decay"]:
-                    p.mul_(1.0 - group["lr"] * group["weight_decay"])
-                upd = O.reshape(p.shape)
-                p.add_(upd, alpha=-lr_eff)
-                contrib[slot] = (upd.pow(2).sum(), lr_eff, upd.numel())
+                contrib[slot] = (ops.muon_update_(p, O, decay, -lr_eff), lr_eff, p.numel())
             start = end
 
     @torch.no_grad()
@@ -118,19 +123,16 @@ class Muon(Optimizer, DiagnosticsMixin):
                         buf = st.get("momentum_buffer")
                         if buf is None:
                             buf = st["momentum_buffer"] = torch.zeros_like(p)
-                        mu = group["momentum"]
-                        buf.mul_(mu).add_(g)
-                        u = g.add(buf, alpha=mu) if group["nesterov"] else buf
-                        u2 = u if u.ndim == 2 else u.reshape(u.shape[0], -1)
-                        key = (tuple(u2.shape), u2.dtype, u2.device)
-                        buckets.setdefault(key, []).append((p, u2, len(contrib)))
+                        # the NS5 input is u reshaped to (rows, -1)
+                        shape2 = tuple(p.shape) if p.ndim == 2 else (p.shape[0], p.numel() // max(p.shape[0], 1))
+                        buckets.setdefault((shape2, p.dtype, p.device), []).append((p, g, buf, len(contrib)))
                         contrib.append(None)
                     else:
                         n_adamw += 1
                         sq, lr_eff = adamw_update(p, g, st, group, want_update_sq=True)
                         contrib.append((sq, lr_eff, p.numel()))
-                for items in buckets.values():
-                    self._orthogonalize_bucket(group, items, contrib)
+                for (shape2, _, _), items in buckets.items():
+                    self._orthogonalize_bucket(group, shape2, items, contrib)
             sq_sum, count = 0.0, 0
             if contrib:
                 by_kind = {}
