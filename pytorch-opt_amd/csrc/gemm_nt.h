@@ -965,7 +965,7 @@ struct TileSet<bf16> {
   // as the 256² tile's; K-FAC Gram and one-matrix NS5 products −1–5%)
   typedef Tile<192, 192, 32, 2, 2, 4, false, 2> sym_mid;
   typedef sym_small sym_tiny;  // unused
-  static constexpr bool kHasMid = true, kHasTiny = false;
+  static constexpr bool kHasMid = true, kHasTiny = false, kMidAll = false;
   static constexpr double kBigRate = 1.5;
   static constexpr double kMidRate = 1.35;
   static constexpr double kTinyRate = 0.0;
@@ -981,22 +981,27 @@ struct TileSet<float> {
   typedef small sym_small;
   typedef Tile<192, 192, 16, 2, 4> sym_mid;
   typedef Tile<32, 32, 16, 2, 2, 8> sym_tiny;
-  static constexpr bool kHasMid = true, kHasTiny = true;
+  static constexpr bool kHasMid = true, kHasTiny = true, kMidAll = false;
   static constexpr double kBigRate = 1.22;
   static constexpr double kMidRate = 1.3;
   static constexpr double kTinyRate = 0.85;
 };
+// fp64 products choose among 128² (8 waves of 64×32), 64² and 32² tiles,
+// symmetric or not: the 128² tile ran the 96 × 2048² per-matrix fp64 roots
+// of a Shampoo refresh 10% faster than 64² (1241–1252 → 1116–1122 ms, same
+// roots; an 8-stage ring or 4×2 waves measured the same), and the 64² tile
+// keeps one-matrix products of 1024–2048 on one round.
 template <>
 struct TileSet<double> {
-  typedef Tile<64, 64, 8, 2, 2> big;
+  typedef Tile<128, 128, 8, 2, 4> big;
   typedef Tile<32, 32, 8, 2, 2> small;
   typedef big sym_big;
   typedef small sym_small;
-  typedef big sym_mid;    // unused
-  typedef small sym_tiny;  // unused
-  static constexpr bool kHasMid = false, kHasTiny = false;
-  static constexpr double kBigRate = 1.25;
-  static constexpr double kMidRate = 0.0;
+  typedef Tile<64, 64, 8, 2, 2> sym_mid;  // the mid tile of every fp64 product
+  typedef small sym_tiny;                 // unused
+  static constexpr bool kHasMid = true, kHasTiny = false, kMidAll = true;
+  static constexpr double kBigRate = 1.39;
+  static constexpr double kMidRate = 1.25;
   static constexpr double kTinyRate = 0.0;
 };
 
@@ -1059,10 +1064,10 @@ struct PickTiles<T, true> {
 // Tiles are spread over the CUs, so the product ends when the busiest CU has
 // run ceil(tiles / CUs) of them. Pick the tile size whose busiest CU covers
 // the least area after weighting each size by its measured rate (small 1.0,
-// big kBigRate, the symmetric 192² tile kMidRate). At the same number of
-// tiles per CU the big tile wins; a big tiling that leaves half the CUs
-// idle (e.g. 64 big tiles against 256 small ones) loses. Returns 0 = small,
-// 1 = big, 2 = mid.
+// big kBigRate, the mid tile kMidRate: symmetric products only, unless the
+// type's kMidAll). At the same number of tiles per CU the big tile wins; a
+// big tiling that leaves half the CUs idle (e.g. 64 big tiles against 256
+// small ones) loses. Returns 0 = small, 1 = big, 2 = mid, 3 = tiny.
 template <typename T, bool UPPER>
 int pick_tile(int64_t M, int64_t N, int64_t batch) {
   typedef typename PickTiles<T, UPPER>::Big Big;
@@ -1081,7 +1086,7 @@ int pick_tile(int64_t M, int64_t N, int64_t batch) {
     best = big;
     pick = 1;
   }
-  if (UPPER && TileSet<T>::kHasMid && load(Mid::BM, Mid::BN, TileSet<T>::kMidRate) < best) {
+  if ((UPPER || TileSet<T>::kMidAll) && TileSet<T>::kHasMid && load(Mid::BM, Mid::BN, TileSet<T>::kMidRate) < best) {
     best = load(Mid::BM, Mid::BN, TileSet<T>::kMidRate);
     pick = 2;
   }
@@ -1107,7 +1112,7 @@ int launch_gemm(const GemmArgs& g, const Epi& epi, int batch, hipStream_t stream
                   (reinterpret_cast<uintptr_t>(g.Q) & 15) == 0,
               std::string(name) + ": operands not 16-byte aligned");
   const int pick = pick_tile<T, UPPER>(g.M, g.N, batch);
-  if constexpr (UPPER && TileSet<T>::kHasMid) {
+  if constexpr ((UPPER || TileSet<T>::kMidAll) && TileSet<T>::kHasMid) {
     typedef typename TileSet<T>::sym_mid Mid;
     static_assert(Mid::BM == Mid::BN && Mid::BK == Big::BK, "mid tile: square, same K tile");
     if (pick == 2) return launch_gemm_cfg<T, Mid, UPPER, Epi, false, false, COMP>(g, epi, batch, stream, name);
