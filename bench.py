@@ -489,7 +489,10 @@ def kernel_probe(torch, ops, hip, dev, which):
              attention matrices: the batched factor update (48 x (L, R),
              beta 0.999) x10, the two-sided apply L·G·R as one batched call
              over the stacked 48 x10, and as 48 single calls (the harness's
-             per-parameter form) x2."""
+             per-parameter form) x2;
+    optimizer  the config-5 Muon step and the Shampoo step (its arm of the
+             set) on seeded gradients, 4 steps each (Shampoo's step 0
+             refreshes the roots, steps 1-3 are plain)."""
     if which == "factors":
         g = torch.Generator(device=dev).manual_seed(2)
         G = 1e-2 * torch.randn(4096, 4096, generator=g, device=dev)
@@ -538,6 +541,27 @@ def kernel_probe(torch, ops, hip, dev, which):
         for _ in range(2):
             for i in range(48):
                 ops.precond_apply_two_sided(Lr[i], Gs[i], Rr[i])
+    elif which == "optimizer":
+        from pytorch_opt import Muon, Shampoo
+
+        mats, vecs = config5_shapes()
+        kind = {n: k for n, _, k in mats}
+        for arm in ("muon", "shampoo"):
+            P = config5_params(torch, dev)
+            rest = [P[n] for n, _ in vecs] + [P["emb"]]
+            if arm == "muon":
+                opt = Muon([{"params": [P[n] for n, _, _ in mats]}, {"params": rest, "use_muon": False}], lr=0.02)
+            else:
+                attn = [P[n] for n, _, _ in mats if kind[n] == "attn"]
+                mlp = [P[n] for n, _, _ in mats if kind[n] == "mlp"]
+                opt = Shampoo([{"params": attn}, {"params": mlp + rest, "use_preconditioner": False, "lr": 3e-4}],
+                              max_preconditioner_dim=4096, precondition_frequency=20, graft="adagrad")
+            for t in range(4):
+                set_grads(torch, P, t, dev)
+                opt.step()
+            torch.cuda.synchronize()
+            del P, opt
+            torch.cuda.empty_cache()
     else:
         raise SystemExit(f"unknown probe {which!r}")
     torch.cuda.synchronize()
@@ -604,7 +628,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="headline only (no factors/roots/optimizer)")
     ap.add_argument("--opt-steps", type=int, default=40)
     ap.add_argument("--traffic-probe", action="store_true", help="one NS5 step + 1 GiB copy, for PMC runs")
-    ap.add_argument("--probe", choices=("factors", "roots", "ns5", "ns5-single", "shampoo"),
+    ap.add_argument("--probe", choices=("factors", "roots", "ns5", "ns5-single", "shampoo", "optimizer"),
                     help="a bounded run of one kernel family for rocprofv3 or a power sampler, no timing")
     ap.add_argument("--digest-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="write the ns5_update HBM traffic summary from two PMC runs")
