@@ -561,11 +561,18 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     return 0;
   };
 
+  // Each recorded event marks a state copy into this thread's pinned slots;
+  // leaving (an error included) waits for it, so no copy lands after the
+  // slots are reused.
   struct Events {
     hipEvent_t e[2] = {nullptr, nullptr};
+    bool recorded[2] = {false, false};
     ~Events() {
-      for (hipEvent_t x : e)
-        if (x) (void)hipEventDestroy(x);
+      for (int i = 0; i < 2; ++i) {
+        if (!e[i]) continue;
+        if (recorded[i]) (void)hipEventSynchronize(e[i]);
+        (void)hipEventDestroy(e[i]);
+      }
     }
   } ev;
   for (hipEvent_t& x : ev.e) PTO_HIP(hipEventCreateWithFlags(&x, hipEventDisableTiming));
@@ -587,6 +594,7 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
     PTO_LAUNCHED("root_decide");
     PTO_HIP(hipMemcpyAsync(hs[k], slot(it - 1), sizeof(RootState<R>), hipMemcpyDeviceToHost, stream));
     PTO_HIP(hipEventRecord(ev.e[k], stream));
+    ev.recorded[k] = true;
     chunk = std::min<int64_t>(chunk * 2, 16);
     return 0;
   };
@@ -599,12 +607,7 @@ int root_t(const TI* A, TI* out, int64_t batch, int64_t n, int64_t p, double dam
       if (ahead && enqueue_chunk(k ^ 1)) return -1;
       PTO_HIP(hipEventSynchronize(ev.e[k]));
       host = *hs[k];
-      if (!ahead || host.stopped) {
-        // a chunk enqueued past a stop only skips (its state is this one);
-        // its copy lands before this thread's buffer can be reused
-        if (ahead) PTO_HIP(hipEventSynchronize(ev.e[k ^ 1]));
-        break;
-      }
+      if (!ahead || host.stopped) break;  // a chunk enqueued past a stop only skips
     }
   }
   const RootState<R>* last = slot(it - 1);  // states after the last iteration run
