@@ -16,11 +16,13 @@
  *    matching *_workspace_bytes query returns, at any alignment (the
  *    library aligns its blocks inside it; the sizes include that slack).
  *    The library never allocates device memory and keeps no state between
- *    calls. A null operand, output or workspace of a non-empty call is an
- *    error reported before any launch.
+ *    calls (the coupled-Newton roots keep two small pinned host slots per
+ *    host thread for their stop state). A null operand, output or
+ *    workspace of a non-empty call is an error reported before any launch.
  *  - `stream` is a hipStream_t; all kernels are enqueued on it and the call
- *    returns without synchronising, except pto_inverse_root, which reads
- *    its stop flag back once per chunk of iterations (the reference syncs
+ *    returns without synchronising, except pto_inverse_root and
+ *    pto_inverse_root_each, which read their stop state back once per chunk
+ *    of iterations, one chunk behind the enqueued work (the reference syncs
  *    once per iteration: csrc/pytorch_opt_ops.cpp:29).
  *  - Return value 0 means success. A non-zero value means failure, and
  *    pto_last_error() returns a message (thread-local).
