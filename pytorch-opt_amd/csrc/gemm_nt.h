@@ -989,8 +989,9 @@ struct TileSet<float> {
 // fp64 products choose among 128² (8 waves of 64×32), 64² and 32² tiles,
 // symmetric or not: the 128² tile ran the 96 × 2048² per-matrix fp64 roots
 // of a Shampoo refresh 10% faster than 64² (1241–1252 → 1116–1122 ms, same
-// roots; an 8-stage ring or 4×2 waves measured the same), and the 64² tile
-// keeps one-matrix products of 1024–2048 on one round.
+// roots; an 8-stage ring or 4×2 waves measured the same); the 64² and 32²
+// tiles keep smaller products on the CUs (a 1024² product on one round of
+// 64² tiles, a symmetric 2048² one on nine of 32²).
 template <>
 struct TileSet<double> {
   typedef Tile<128, 128, 8, 2, 4> big;

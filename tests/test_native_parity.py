@@ -272,6 +272,7 @@ def test_kron_nonsymmetric_prior_and_fp64(native_backend, m, n):
     (torch.float32, 2, 4096, 4096, 0.95),   # single calls: one round of 192² tiles in the searched order
     (torch.float32, 70, 96, 64, 1.0),       # two launches (64 per call), plain sums
     (torch.float64, 6, 130, 257, 0.9),
+    (torch.float64, 16, 2048, 2048, 0.999),  # batched on 128² tiles, single calls on 32²
 ])
 def test_kron_batched_matches_single_calls(native_backend, hip, dtype, k, m, n, beta2):
     """One kron_factor_update_batched_ call gives every factor exactly the
@@ -293,6 +294,43 @@ def test_kron_batched_matches_single_calls(native_backend, hip, dtype, k, m, n, 
     assert hip.prof_query("kron_left")[1] == (k + 63) // 64
     for i in range(k):
         assert torch.equal(Ls[i], L1[i]) and torch.equal(Rs[i], R1[i]), i
+
+
+def _fp64_pick(m, n, batch, upper):
+    """Tile edge the per-CU load model picks for an fp64 product (128, 64 or
+    32): rounds of tiles over the CUs times the tile area over its rate."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    best = None
+    for edge, rate in ((32, 1.0), (128, 1.39), (64, 1.25)):
+        tm, tn = -(-m // edge), -(-n // edge)
+        tiles = (tm * (tm + 1) // 2 if upper else tm * tn) * batch
+        load = -(-tiles // cus) * edge * edge / rate
+        if best is None or load < best[0]:
+            best = (load, edge)
+    return best[1]
+
+
+def test_fp64_big_tile_products_vs_torch(native_backend):
+    """fp64 products on the 128² tile (8 waves of 64×32): a batched two-sided
+    product 8 × 1024² (non-symmetric launches) and a batched factor update
+    16 × 2048² (symmetric, upper tiles mirrored) against torch's float64
+    matmul."""
+    assert _fp64_pick(1024, 1024, 8, False) == 128 and _fp64_pick(2048, 2048, 16, True) == 128
+    assert _fp64_pick(2048, 2048, 1, True) == 32  # the single calls the kron test compares with
+    g = torch.Generator(device=DEV).manual_seed(21)
+    A, X, B = (torch.randn(8, 1024, 1024, generator=g, device=DEV, dtype=torch.float64) for _ in range(3))
+    got = ops.two_sided_product(A, X, B)
+    want = torch.matmul(torch.matmul(A, X), B)
+    assert float((got - want).norm() / want.norm()) < 1e-13
+    Gs = [torch.randn(2048, 2048, generator=g, device=DEV, dtype=torch.float64) for _ in range(16)]
+    Ls = [torch.zeros(2048, 2048, device=DEV, dtype=torch.float64) for _ in range(16)]
+    Rs = [torch.zeros(2048, 2048, device=DEV, dtype=torch.float64) for _ in range(16)]
+    ops.kron_factor_update_batched_(Ls, Rs, Gs, beta2=1.0)
+    for i in (0, 7, 15):
+        wl, wr = Gs[i] @ Gs[i].T, Gs[i].T @ Gs[i]
+        assert float((Ls[i] - wl).norm() / wl.norm()) < 1e-13, i
+        assert float((Rs[i] - wr).norm() / wr.norm()) < 1e-13, i
+        assert torch.equal(Ls[i], Ls[i].T) and torch.equal(Rs[i], Rs[i].T), i
 
 
 def test_kron_batched_byte_cap(native_backend, hip, monkeypatch):
